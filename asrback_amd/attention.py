@@ -1,0 +1,415 @@
+"""Attention ops on the HIP kernels of ``libasrattn.so``.
+
+These take PyTorch tensors (often strided views: heads split out of a fused
+projection, slices of a preallocated cache), pass their device pointers and
+element strides to the C ABI, and launch on the current HIP stream, so they
+can run inside ``torch.cuda.graph`` capture (a hipGraph on ROCm).  Nothing
+here synchronizes with the device.
+
+Three entry points cover every attention call of the reference:
+
+* :func:`sdpa` -- ``F.scaled_dot_product_attention`` as the reference calls
+  it, on ``(batch, heads, length, head_dim)`` tensors, with the masks it
+  builds expressed as key counts (:class:`KeyPrefix`).  Rows with one query
+  go to the decode kernel, longer ones to the multi-row kernel.
+* :func:`varlen_attn` -- ``torch.nn.attention.varlen.varlen_attn`` with the
+  arguments the reference passes (``seqused_k``, ``window_size``,
+  ``enable_gqa``, ``num_splits``).
+* :func:`decode` -- one query per sequence over a key/value cache, any
+  strides (the Whisper ``(B, H, L, D)`` and Qwen3 ``(B, L, H_kv, D)``
+  caches).
+
+The reference's masks are all prefix masks: each query row sees keys
+``0 .. n-1`` (optionally causal on top).  General boolean masks are not
+supported.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+from dataclasses import dataclass
+
+import torch
+from torch import Tensor
+
+from . import _lib
+
+_DTYPES = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16}
+
+
+@dataclass(frozen=True)
+class KeyPrefix:
+    """A key mask that shows each row the keys ``0 .. n_b - 1``.
+
+    ``n_b = positions[b] + 1`` (int64 ``positions``, the Whisper decoder step,
+    ``whisper.py:263-264``) or ``n_b = lengths[b]`` (int32 ``lengths``, the
+    padding masks of ``sensevoice.py:548-550`` and ``qwen3_asr.py:510-515``).
+    Both stay on the device, so a captured graph sees their new values on
+    every replay.
+    """
+
+    positions: Tensor | None = None
+    lengths: Tensor | None = None
+
+    def __post_init__(self) -> None:
+        if (self.positions is None) == (self.lengths is None):
+            raise ValueError("KeyPrefix takes exactly one of positions and lengths")
+        if self.positions is not None and self.positions.dtype != torch.int64:
+            raise TypeError(f"positions must be int64, got {self.positions.dtype}")
+        if self.lengths is not None and self.lengths.dtype != torch.int32:
+            raise TypeError(f"lengths must be int32, got {self.lengths.dtype}")
+
+    @classmethod
+    def from_mask(cls, mask: Tensor) -> KeyPrefix:
+        """The prefix described by a boolean ``(batch, 1, 1, length)`` or
+        ``(batch, length)`` mask that is True for keys ``0 .. n_b - 1``."""
+        if mask.dtype != torch.bool:
+            raise TypeError(f"only boolean prefix masks are supported, got {mask.dtype}")
+        lengths = mask.reshape(mask.shape[0], mask.shape[-1]).sum(dim=-1, dtype=torch.int32)
+        return cls(lengths=lengths)
+
+
+def _dtype_code(*tensors: Tensor) -> int:
+    dtype = tensors[0].dtype
+    if dtype not in _DTYPES:
+        raise TypeError(f"attention supports float32 and bfloat16, got {dtype}")
+    for tensor in tensors:
+        if tensor.dtype != dtype:
+            raise TypeError(f"mixed dtypes: {dtype} and {tensor.dtype}")
+        if tensor.device.type != "cuda":
+            raise RuntimeError(
+                f"attention kernels run on the GPU only; got a tensor on {tensor.device}"
+            )
+    return _DTYPES[dtype]
+
+
+def _aligned(t: Tensor, dims: tuple[int, ...]) -> Tensor:
+    """``t`` itself when its rows can be read with 16-byte vectors, else a
+    contiguous copy.  ``dims`` are the strided (non head_dim) axes."""
+    per_vec = 16 // t.element_size()
+    if (
+        t.stride(-1) == 1
+        and t.data_ptr() % 16 == 0
+        and all(t.stride(d) % per_vec == 0 for d in dims)
+    ):
+        return t
+    return t.contiguous()
+
+
+def _ptr(t: Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _check_device(*tensors: Tensor | None) -> torch.device:
+    device = None
+    for tensor in tensors:
+        if tensor is None:
+            continue
+        if device is None:
+            device = tensor.device
+        elif tensor.device != device:
+            raise RuntimeError(f"tensors on different devices: {device} and {tensor.device}")
+    if device.index is not None and device.index != torch.cuda.current_device():
+        raise RuntimeError(
+            f"tensors are on {device} but the current device is cuda:{torch.cuda.current_device()}"
+        )
+    return device
+
+
+def _int32(t: Tensor | None, name: str) -> Tensor | None:
+    if t is None:
+        return None
+    if t.dtype != torch.int32:
+        raise TypeError(f"{name} must be int32, got {t.dtype}")
+    return t.contiguous()
+
+
+def flash(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    *,
+    out: Tensor | None = None,
+    causal: int = _lib.CAUSAL_NONE,
+    cu_seqlens_q: Tensor | None = None,
+    cu_seqlens_k: Tensor | None = None,
+    max_len_q: int | None = None,
+    max_len_k: int | None = None,
+    seqused_k: Tensor | None = None,
+    scale: float | None = None,
+    force_valu: bool = False,
+) -> Tensor:
+    """Multi-row attention (``asrattn_fwd``).
+
+    Padded layout: ``q`` ``(batch, len_q, heads_q, head_dim)``, ``k``/``v``
+    ``(batch, len_k, heads_kv, head_dim)``; packed layout (``cu_seqlens_*``
+    given): ``(tokens, heads, head_dim)``.  Returns ``out`` in ``q``'s layout
+    (a new contiguous tensor unless ``out`` is given).
+    """
+    dtype = _dtype_code(q, k, v)
+    packed = cu_seqlens_q is not None
+    if packed != (cu_seqlens_k is not None):
+        raise ValueError("cu_seqlens_q and cu_seqlens_k go together")
+    rank = 3 if packed else 4
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        if t.dim() != rank:
+            raise ValueError(f"{name} must have {rank} dimensions, got shape {tuple(t.shape)}")
+    if k.shape != v.shape:
+        raise ValueError(f"k and v shapes differ: {tuple(k.shape)} vs {tuple(v.shape)}")
+    head_dim = q.shape[-1]
+    heads_q, heads_kv = q.shape[-2], k.shape[-2]
+    if k.shape[-1] != head_dim:
+        raise ValueError("q and k head_dim differ")
+    if heads_q % heads_kv:
+        raise ValueError(f"{heads_q} query heads are not a multiple of {heads_kv} kv heads")
+    strided = (0, 1, 2) if not packed else (0, 1)
+    q, k, v = (_aligned(t, strided) for t in (q, k, v))
+    if out is None:
+        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    elif out.shape != q.shape or out.dtype != q.dtype:
+        raise ValueError("out must match q's shape and dtype")
+    device = _check_device(q, k, v, out, cu_seqlens_q, cu_seqlens_k, seqused_k)
+    cu_seqlens_q = _int32(cu_seqlens_q, "cu_seqlens_q")
+    cu_seqlens_k = _int32(cu_seqlens_k, "cu_seqlens_k")
+    seqused_k = _int32(seqused_k, "seqused_k")
+
+    params = _lib.FwdParams()
+    params.q, params.k, params.v, params.out = q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr()
+    if packed:
+        if max_len_q is None or max_len_k is None:
+            raise ValueError("packed sequences need max_len_q and max_len_k")
+        batch = cu_seqlens_q.shape[0] - 1
+        if cu_seqlens_k.shape[0] != batch + 1:
+            raise ValueError("cu_seqlens_q and cu_seqlens_k have different lengths")
+        for prefix, t in (("q", q), ("k", k), ("v", v), ("o", out)):
+            setattr(params, f"{prefix}_batch_stride", 0)
+            setattr(params, f"{prefix}_token_stride", t.stride(0))
+            setattr(params, f"{prefix}_head_stride", t.stride(1))
+    else:
+        batch = q.shape[0]
+        if k.shape[0] != batch:
+            raise ValueError("q and k batch sizes differ")
+        max_len_q = q.shape[1] if max_len_q is None else max_len_q
+        max_len_k = k.shape[1] if max_len_k is None else max_len_k
+        if max_len_q > q.shape[1] or max_len_k > k.shape[1]:
+            raise ValueError("max_len_q / max_len_k exceed the tensors")
+        for prefix, t in (("q", q), ("k", k), ("v", v), ("o", out)):
+            setattr(params, f"{prefix}_batch_stride", t.stride(0))
+            setattr(params, f"{prefix}_token_stride", t.stride(1))
+            setattr(params, f"{prefix}_head_stride", t.stride(2))
+    if seqused_k is not None and seqused_k.shape[0] != batch:
+        raise ValueError(f"seqused_k has {seqused_k.shape[0]} entries for {batch} sequences")
+    params.cu_seqlens_q = _ptr(cu_seqlens_q)
+    params.cu_seqlens_k = _ptr(cu_seqlens_k)
+    params.seqused_k = _ptr(seqused_k)
+    params.batch = batch
+    params.heads_q = heads_q
+    params.heads_kv = heads_kv
+    params.head_dim = head_dim
+    params.max_len_q = max_len_q
+    params.max_len_k = max_len_k
+    params.causal = causal
+    params.dtype = dtype
+    params.scale = 1.0 / math.sqrt(head_dim) if scale is None else scale
+    params.flags = _lib.FWD_FORCE_VALU if force_valu else 0
+    lib = _lib.load()
+    _lib.check(lib.asrattn_fwd(ctypes.byref(params), _stream(device)), "asrattn_fwd")
+    return out
+
+
+def _decode_params(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    out: Tensor,
+    seqused_k: Tensor | None,
+    positions: Tensor | None,
+    num_splits: int,
+    scale: float | None,
+) -> _lib.DecodeParams:
+    params = _lib.DecodeParams()
+    params.q, params.k, params.v, params.out = q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr()
+    params.q_batch_stride, params.q_head_stride = q.stride(0), q.stride(1)
+    params.k_batch_stride, params.k_token_stride, params.k_head_stride = k.stride(0), k.stride(1), k.stride(2)
+    params.v_batch_stride, params.v_token_stride, params.v_head_stride = v.stride(0), v.stride(1), v.stride(2)
+    params.o_batch_stride, params.o_head_stride = out.stride(0), out.stride(1)
+    params.seqused_k = _ptr(seqused_k)
+    params.positions = _ptr(positions)
+    params.batch = q.shape[0]
+    params.heads_q = q.shape[1]
+    params.heads_kv = k.shape[2]
+    params.head_dim = q.shape[2]
+    params.max_len_k = k.shape[1]
+    params.num_splits = num_splits
+    params.dtype = _dtype_code(q, k, v)
+    params.scale = 1.0 / math.sqrt(q.shape[2]) if scale is None else scale
+    return params
+
+
+def decode(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    *,
+    seqused_k: Tensor | None = None,
+    positions: Tensor | None = None,
+    num_splits: int = 0,
+    scale: float | None = None,
+    out: Tensor | None = None,
+) -> Tensor:
+    """One query per sequence over a cache (``asrattn_decode``).
+
+    ``q`` ``(batch, heads_q, head_dim)``; ``k``/``v`` ``(batch, length,
+    heads_kv, head_dim)``, any strides with a unit last one (pass
+    ``cache.transpose(1, 2)`` for a ``(batch, heads, length, head_dim)``
+    cache).  Sequence ``b`` uses keys ``0 .. n_b - 1`` with ``n_b =
+    seqused_k[b]`` (int32), ``positions[b] + 1`` (int64) or ``length``.
+    Returns ``(batch, heads_q, head_dim)``.
+    """
+    if q.dim() != 3 or k.dim() != 4 or v.shape != k.shape:
+        raise ValueError(
+            f"decode expects q (B, Hq, D) and k/v (B, L, Hkv, D); got {tuple(q.shape)}, "
+            f"{tuple(k.shape)}, {tuple(v.shape)}"
+        )
+    if k.shape[0] != q.shape[0] or k.shape[3] != q.shape[2]:
+        raise ValueError("q and k disagree on batch or head_dim")
+    if q.shape[1] % k.shape[2]:
+        raise ValueError(f"{q.shape[1]} query heads are not a multiple of {k.shape[2]} kv heads")
+    _dtype_code(q, k, v)
+    q = _aligned(q, (0, 1))
+    k, v = (_aligned(t, (0, 1, 2)) for t in (k, v))
+    if out is None:
+        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    elif out.shape != q.shape or out.dtype != q.dtype or out.stride(-1) != 1:
+        raise ValueError("out must match q's shape and dtype, with a unit last stride")
+    if seqused_k is not None:
+        seqused_k = _int32(seqused_k, "seqused_k")
+    if positions is not None:
+        if positions.dtype != torch.int64:
+            raise TypeError(f"positions must be int64, got {positions.dtype}")
+        positions = positions.contiguous()
+    for lengths in (seqused_k, positions):
+        if lengths is not None and lengths.shape != (q.shape[0],):
+            raise ValueError(f"key counts must have shape ({q.shape[0]},), got {tuple(lengths.shape)}")
+    device = _check_device(q, k, v, out, seqused_k, positions)
+    params = _decode_params(q, k, v, out, seqused_k, positions, num_splits, scale)
+    lib = _lib.load()
+    need = lib.asrattn_decode_workspace_size(ctypes.byref(params))
+    if need == ctypes.c_size_t(-1).value:
+        _lib.check(lib.asrattn_decode(ctypes.byref(params), None, 0, _stream(device)), "asrattn_decode")
+    workspace = None
+    if need:
+        workspace = torch.empty(need, dtype=torch.uint8, device=device)
+    _lib.check(
+        lib.asrattn_decode(
+            ctypes.byref(params), _ptr(workspace), need, _stream(device)
+        ),
+        "asrattn_decode",
+    )
+    return out
+
+
+def sdpa(
+    query: Tensor,
+    key: Tensor,
+    value: Tensor,
+    mask: KeyPrefix | Tensor | None = None,
+    is_causal: bool = False,
+    *,
+    enable_gqa: bool = False,
+    scale: float | None = None,
+) -> Tensor:
+    """``F.scaled_dot_product_attention(query, key, value, attn_mask=mask,
+    is_causal=is_causal, enable_gqa=enable_gqa)`` for ``(batch, heads,
+    length, head_dim)`` tensors, with ``mask`` a :class:`KeyPrefix` or a
+    boolean prefix mask.  ``is_causal`` is top-left aligned, as in torch.
+
+    Returns the output as ``(batch, length_q, heads, head_dim)`` -- the
+    layout the callers reshape to ``(batch, length_q, width)`` next -- so no
+    transpose copy is needed.
+    """
+    if query.dim() != 4 or key.dim() != 4 or value.shape != key.shape:
+        raise ValueError("sdpa expects 4-d (batch, heads, length, head_dim) tensors")
+    if query.shape[1] != key.shape[1] and not enable_gqa:
+        raise ValueError("query and key head counts differ; pass enable_gqa=True")
+    if isinstance(mask, Tensor):
+        mask = KeyPrefix.from_mask(mask)
+    q = query.transpose(1, 2)
+    k = key.transpose(1, 2)
+    v = value.transpose(1, 2)
+    batch, len_q, heads, head_dim = q.shape
+    if len_q == 1:
+        # One query per row: the split-K decode kernel.  A causal single query
+        # sees key 0 only (top-left alignment).
+        out = torch.empty((batch, 1, heads, head_dim), dtype=q.dtype, device=q.device)
+        if is_causal:
+            k, v = k[:, :1], v[:, :1]
+        decode(
+            q[:, 0],
+            k,
+            v,
+            seqused_k=None if mask is None else mask.lengths,
+            positions=None if mask is None else mask.positions,
+            scale=scale,
+            out=out[:, 0],
+        )
+        return out
+    seqused = None
+    if mask is not None:
+        seqused = mask.lengths
+        if seqused is None:
+            seqused = (mask.positions + 1).clamp(max=k.shape[1]).to(torch.int32)
+    return flash(
+        q,
+        k,
+        v,
+        causal=_lib.CAUSAL_TOP_LEFT if is_causal else _lib.CAUSAL_NONE,
+        seqused_k=seqused,
+        scale=scale,
+    )
+
+
+def varlen_attn(
+    query: Tensor,
+    key: Tensor,
+    value: Tensor,
+    cu_seq_q: Tensor,
+    cu_seq_k: Tensor,
+    max_q: int,
+    max_k: int,
+    *,
+    window_size: tuple[int, int] = (-1, -1),
+    enable_gqa: bool = False,
+    seqused_k: Tensor | None = None,
+    num_splits: int | None = None,
+    scale: float | None = None,
+) -> Tensor:
+    """``torch.nn.attention.varlen.varlen_attn`` with the arguments the
+    reference uses (``sensevoice.py:115-125``, ``qwen3_asr.py:156-166``,
+    ``qwen3_asr.py:414-425``): packed ``(tokens, heads, head_dim)`` tensors,
+    int32 cumulative sequence starts, ``window_size=(-1, 0)`` for causal
+    (bottom-right aligned) and ``(-1, -1)`` for none.  ``num_splits`` is a
+    tuning hint of the flash kernel and has no effect here.
+    """
+    del num_splits
+    if window_size not in ((-1, -1), (-1, 0)):
+        raise ValueError(f"window_size {window_size} is not supported (only (-1, -1) and (-1, 0))")
+    if query.shape[1] != key.shape[1] and not enable_gqa:
+        raise ValueError("query and key head counts differ; pass enable_gqa=True")
+    return flash(
+        query,
+        key,
+        value,
+        causal=_lib.CAUSAL_BOTTOM_RIGHT if window_size == (-1, 0) else _lib.CAUSAL_NONE,
+        cu_seqlens_q=cu_seq_q,
+        cu_seqlens_k=cu_seq_k,
+        max_len_q=max_q,
+        max_len_k=max_k,
+        seqused_k=seqused_k,
+        scale=scale,
+    )

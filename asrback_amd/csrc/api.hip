@@ -1,0 +1,170 @@
+// C ABI of the attention library: argument checks, kernel choice, launch and
+// error reporting.  Nothing here allocates device memory or synchronizes, so
+// every entry point can run inside HIP graph capture.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <cmath>
+#include <string>
+
+#include "asrattn.h"
+#include "kernels.hpp"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int ok() {
+  g_last_error.clear();
+  return ASRATTN_OK;
+}
+
+int elem_bytes(int dtype) { return dtype == ASRATTN_BF16 ? 2 : 4; }
+
+// 16-byte vector access needs 16-byte aligned rows: pointer aligned and every
+// stride a multiple of one vector.
+bool vec_aligned(const void* ptr, int dtype, std::initializer_list<int64_t> strides) {
+  if ((reinterpret_cast<uintptr_t>(ptr) & 15u) != 0) return false;
+  const int64_t per_vec = 16 / elem_bytes(dtype);
+  for (int64_t s : strides)
+    if (s % per_vec != 0) return false;
+  return true;
+}
+
+int check_common(int dtype, int heads_q, int heads_kv, int head_dim, float scale) {
+  if (dtype != ASRATTN_F32 && dtype != ASRATTN_BF16)
+    return fail(ASRATTN_ERR_INVALID, "dtype %d is neither ASRATTN_F32 nor ASRATTN_BF16", dtype);
+  if (heads_q <= 0 || heads_kv <= 0 || heads_q % heads_kv != 0)
+    return fail(ASRATTN_ERR_INVALID, "heads_q (%d) must be a positive multiple of heads_kv (%d)", heads_q,
+                heads_kv);
+  if (head_dim <= 0) return fail(ASRATTN_ERR_INVALID, "head_dim must be positive, got %d", head_dim);
+  if (!(scale > 0.f) || !std::isfinite(scale))
+    return fail(ASRATTN_ERR_INVALID, "scale must be positive and finite, got %g", (double)scale);
+  return ASRATTN_OK;
+}
+
+int from_hip(hipError_t err, const char* what) {
+  if (err == hipSuccess) return ok();
+  return fail(ASRATTN_ERR_HIP, "%s: %s", what, hipGetErrorString(err));
+}
+
+int decode_splits(const asrattn_decode_params& p) {
+  if (p.num_splits > 0) return p.num_splits;
+  // About four workgroups per CU (256 CUs) in flight, but at least 128 keys
+  // per split so a split streams whole load batches.
+  const long long pairs = (long long)p.batch * p.heads_kv;
+  long long s = (1024 + pairs - 1) / pairs;
+  const long long by_len = (p.max_len_k + 127) / 128;
+  if (s > by_len) s = by_len;
+  if (s > 64) s = 64;
+  if (s < 1) s = 1;
+  return (int)s;
+}
+
+int check_decode(const asrattn_decode_params* p) {
+  if (p == nullptr) return fail(ASRATTN_ERR_INVALID, "params is NULL");
+  int rc = check_common(p->dtype, p->heads_q, p->heads_kv, p->head_dim, p->scale);
+  if (rc != ASRATTN_OK) return rc;
+  if (p->batch < 0) return fail(ASRATTN_ERR_INVALID, "batch must be >= 0, got %d", p->batch);
+  if (p->max_len_k < 0) return fail(ASRATTN_ERR_INVALID, "max_len_k must be >= 0, got %d", p->max_len_k);
+  if (p->num_splits < 0 || p->num_splits > 1024)
+    return fail(ASRATTN_ERR_INVALID, "num_splits must be in [0, 1024], got %d", p->num_splits);
+  const int group = p->heads_q / p->heads_kv;
+  if (!asrattn::decode_supported(p->dtype, p->head_dim, group))
+    return fail(ASRATTN_ERR_UNSUPPORTED,
+                "no decode kernel for head_dim %d with %d query heads per kv head (supported: head_dim "
+                "64/128, 1/2/4 heads per kv head)",
+                p->head_dim, group);
+  return ASRATTN_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* asrattn_last_error(void) { return g_last_error.c_str(); }
+
+int asrattn_abi_version(void) { return ASRATTN_ABI_VERSION; }
+
+int asrattn_fwd(const asrattn_fwd_params* params, void* stream) {
+  if (params == nullptr) return fail(ASRATTN_ERR_INVALID, "params is NULL");
+  const asrattn_fwd_params& p = *params;
+  int rc = check_common(p.dtype, p.heads_q, p.heads_kv, p.head_dim, p.scale);
+  if (rc != ASRATTN_OK) return rc;
+  if (p.batch < 0 || p.max_len_q < 0 || p.max_len_k < 0)
+    return fail(ASRATTN_ERR_INVALID, "batch (%d), max_len_q (%d) and max_len_k (%d) must be >= 0", p.batch,
+                p.max_len_q, p.max_len_k);
+  if (p.causal < ASRATTN_CAUSAL_NONE || p.causal > ASRATTN_CAUSAL_BOTTOM_RIGHT)
+    return fail(ASRATTN_ERR_INVALID, "causal must be 0, 1 or 2, got %d", p.causal);
+  if ((p.cu_seqlens_q == nullptr) != (p.cu_seqlens_k == nullptr))
+    return fail(ASRATTN_ERR_INVALID, "cu_seqlens_q and cu_seqlens_k must both be set or both be NULL");
+  if (p.batch == 0 || p.max_len_q == 0) return ok();
+  if (p.q == nullptr || p.k == nullptr || p.v == nullptr || p.out == nullptr)
+    return fail(ASRATTN_ERR_INVALID, "q, k, v and out must be non-NULL");
+  if (!vec_aligned(p.q, p.dtype, {p.q_batch_stride, p.q_token_stride, p.q_head_stride}) ||
+      !vec_aligned(p.k, p.dtype, {p.k_batch_stride, p.k_token_stride, p.k_head_stride}) ||
+      !vec_aligned(p.v, p.dtype, {p.v_batch_stride, p.v_token_stride, p.v_head_stride}) ||
+      !vec_aligned(p.out, p.dtype, {p.o_batch_stride, p.o_token_stride, p.o_head_stride}))
+    return fail(ASRATTN_ERR_INVALID,
+                "q, k, v and out need 16-byte aligned pointers and strides that are multiples of 16 bytes");
+  const bool generic = (p.flags & ASRATTN_FWD_FORCE_VALU) != 0;
+  if (!generic && asrattn::fwd_mfma_supported(p.dtype, p.head_dim))
+    return from_hip(asrattn::launch_fwd_mfma(p, static_cast<hipStream_t>(stream)), "asrattn_fwd (mfma)");
+  if (asrattn::fwd_valu_supported(p.dtype, p.head_dim))
+    return from_hip(asrattn::launch_fwd_valu(p, static_cast<hipStream_t>(stream)), "asrattn_fwd (valu)");
+  return fail(ASRATTN_ERR_UNSUPPORTED, "no forward kernel for head_dim %d (supported: 64, 128)", p.head_dim);
+}
+
+int asrattn_decode_num_splits(const asrattn_decode_params* params) {
+  if (check_decode(params) != ASRATTN_OK) return -1;
+  return decode_splits(*params);
+}
+
+size_t asrattn_decode_workspace_size(const asrattn_decode_params* params) {
+  if (check_decode(params) != ASRATTN_OK) return (size_t)-1;
+  const asrattn_decode_params& p = *params;
+  const int s = decode_splits(p);
+  if (s == 1) return 0;
+  const size_t rows = (size_t)p.batch * p.heads_q * s;
+  return rows * (size_t)p.head_dim * sizeof(float) + rows * 2 * sizeof(float);
+}
+
+int asrattn_decode(const asrattn_decode_params* params, void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_decode(params);
+  if (rc != ASRATTN_OK) return rc;
+  const asrattn_decode_params& p = *params;
+  if (p.batch == 0) return ok();
+  if (p.q == nullptr || p.k == nullptr || p.v == nullptr || p.out == nullptr)
+    return fail(ASRATTN_ERR_INVALID, "q, k, v and out must be non-NULL");
+  if (!vec_aligned(p.q, p.dtype, {p.q_batch_stride, p.q_head_stride}) ||
+      !vec_aligned(p.k, p.dtype, {p.k_batch_stride, p.k_token_stride, p.k_head_stride}) ||
+      !vec_aligned(p.v, p.dtype, {p.v_batch_stride, p.v_token_stride, p.v_head_stride}))
+    return fail(ASRATTN_ERR_INVALID,
+                "q, k and v need 16-byte aligned pointers and strides that are multiples of 16 bytes");
+  const int s = decode_splits(p);
+  const size_t need = asrattn_decode_workspace_size(params);
+  float* ws_o = nullptr;
+  float* ws_ml = nullptr;
+  if (s > 1) {
+    if (workspace == nullptr || workspace_bytes < need)
+      return fail(ASRATTN_ERR_WORKSPACE, "decode needs %zu workspace bytes, got %zu", need,
+                  workspace == nullptr ? (size_t)0 : workspace_bytes);
+    if ((reinterpret_cast<uintptr_t>(workspace) & 15u) != 0)
+      return fail(ASRATTN_ERR_WORKSPACE, "workspace must be 16-byte aligned");
+    ws_o = static_cast<float*>(workspace);
+    ws_ml = ws_o + (size_t)p.batch * p.heads_q * s * p.head_dim;
+  }
+  return from_hip(asrattn::launch_decode(p, s, ws_o, ws_ml, static_cast<hipStream_t>(stream)), "asrattn_decode");
+}
+
+}  // extern "C"

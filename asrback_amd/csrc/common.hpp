@@ -1,0 +1,96 @@
+// Device helpers shared by the attention kernels (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "asrattn.h"
+
+namespace asrattn {
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kNegInf = -__builtin_inff();
+
+// bf16 is carried as raw 16-bit storage; the kernels convert explicitly.
+using bf16_raw = uint16_t;
+
+__device__ __forceinline__ float bf16_lo(uint32_t pair) { return __uint_as_float(pair << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t pair) { return __uint_as_float(pair & 0xffff0000u); }
+__device__ __forceinline__ float bf16_to_f32(bf16_raw x) { return __uint_as_float((uint32_t)x << 16); }
+
+// Round-to-nearest-even fp32 -> bf16 pair; gfx950 does this in one
+// v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  bf16x2_t r;
+  r.x = (__bf16)lo;
+  r.y = (__bf16)hi;
+  return __builtin_bit_cast(uint32_t, r);
+}
+__device__ __forceinline__ bf16_raw f32_to_bf16(float x) {
+  return (bf16_raw)(pack_bf16x2(x, 0.f) & 0xffffu);
+}
+
+// 2^x on the hardware exponential unit (v_exp_f32).
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Element type traits: 16-byte vector loads, converted to fp32.
+template <typename T>
+struct Elem;
+
+template <>
+struct Elem<float> {
+  static constexpr int kPerVec = 4;  // elements per 16-byte load
+  static __device__ __forceinline__ void load16(const float* p, float* out) {
+    const float4 v = *reinterpret_cast<const float4*>(p);
+    out[0] = v.x; out[1] = v.y; out[2] = v.z; out[3] = v.w;
+  }
+  static __device__ __forceinline__ float load1(const float* p) { return *p; }
+  static __device__ __forceinline__ void store1(float* p, float x) { *p = x; }
+};
+
+template <>
+struct Elem<bf16_raw> {
+  static constexpr int kPerVec = 8;
+  static __device__ __forceinline__ void load16(const bf16_raw* p, float* out) {
+    const uint4 v = *reinterpret_cast<const uint4*>(p);
+    out[0] = bf16_lo(v.x); out[1] = bf16_hi(v.x);
+    out[2] = bf16_lo(v.y); out[3] = bf16_hi(v.y);
+    out[4] = bf16_lo(v.z); out[5] = bf16_hi(v.z);
+    out[6] = bf16_lo(v.w); out[7] = bf16_hi(v.w);
+  }
+  static __device__ __forceinline__ float load1(const bf16_raw* p) { return bf16_to_f32(*p); }
+  static __device__ __forceinline__ void store1(bf16_raw* p, float x) { *p = f32_to_bf16(x); }
+};
+
+// Butterfly reductions inside aligned groups of W lanes (W a power of two
+// <= 64); every lane of the group ends with the result.
+template <int W>
+__device__ __forceinline__ float group_sum(float x) {
+#pragma unroll
+  for (int off = W / 2; off > 0; off >>= 1) x += __shfl_xor(x, off, 64);
+  return x;
+}
+template <int W>
+__device__ __forceinline__ float group_max(float x) {
+#pragma unroll
+  for (int off = W / 2; off > 0; off >>= 1) x = fmaxf(x, __shfl_xor(x, off, 64));
+  return x;
+}
+
+// Keys sequence b uses in a decoder step: seqused_k, else positions + 1,
+// else all of them; clamped to [0, max_len].
+__device__ __forceinline__ int decode_key_count(const int32_t* seqused, const int64_t* positions,
+                                                int b, int max_len) {
+  long long n = max_len;
+  if (seqused != nullptr) {
+    n = seqused[b];
+  } else if (positions != nullptr) {
+    n = positions[b] + 1;
+  }
+  if (n > max_len) n = max_len;
+  if (n < 0) n = 0;
+  return (int)n;
+}
+
+}  // namespace asrattn

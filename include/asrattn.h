@@ -1,0 +1,183 @@
+/*
+ * asrattn.h -- C ABI of the MI355X (gfx950) attention library behind the
+ * asrback attention modules.
+ *
+ * The reference (sjjeong94/asrback) has no native code and no FFI: its
+ * attention is reached through two PyTorch ops called from plain-PyTorch
+ * modules.  Every entry point below replaces a group of those op calls; the
+ * reference call sites are cited as path:line relative to the reference repo.
+ *
+ * Conventions
+ *   - Tensors are passed as device pointers plus element strides (elements,
+ *     not bytes).  The head_dim axis must have unit stride; every other axis
+ *     may be strided (views of fused projections, cache slices, ...).
+ *   - dtype is ASRATTN_F32 or ASRATTN_BF16 and applies to q, k, v and out.
+ *     Arithmetic is always fp32 (bf16 operands, fp32 accumulation).
+ *   - Per-sequence lengths live in device memory, so a call can be captured
+ *     in a HIP graph and replayed while the lengths change.
+ *   - stream is a hipStream_t (passed as void*); every launch goes there.
+ *   - No entry point allocates device memory or synchronizes.  Scratch space
+ *     comes from the caller (asrattn_decode's workspace).
+ *   - Every entry point returns ASRATTN_OK (0) or an error code; the message
+ *     of the last error on the calling thread is asrattn_last_error().
+ *     Nothing aborts the process.
+ */
+#ifndef ASRATTN_H
+#define ASRATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ASRATTN_ABI_VERSION 1
+
+enum asrattn_status {
+  ASRATTN_OK = 0,
+  ASRATTN_ERR_INVALID = 1,      /* bad argument (shape, stride, pointer) */
+  ASRATTN_ERR_UNSUPPORTED = 2,  /* valid request this build has no kernel for */
+  ASRATTN_ERR_HIP = 3,          /* the HIP runtime reported an error */
+  ASRATTN_ERR_WORKSPACE = 4     /* workspace missing or too small */
+};
+
+enum asrattn_dtype { ASRATTN_F32 = 0, ASRATTN_BF16 = 1 };
+
+/* asrattn_fwd_params.flags: run the fp32 vector-ALU kernel even where the
+   bf16 matrix-core kernel applies (the exact-arithmetic twin, for checks). */
+#define ASRATTN_FWD_FORCE_VALU 1
+
+enum asrattn_causal {
+  ASRATTN_CAUSAL_NONE = 0,
+  /* query i sees keys j <= i (torch SDPA is_causal=True, top-left aligned) */
+  ASRATTN_CAUSAL_TOP_LEFT = 1,
+  /* query i sees keys j <= i + (keys - queries) (flash varlen
+     window_size=(-1, 0), bottom-right aligned) */
+  ASRATTN_CAUSAL_BOTTOM_RIGHT = 2
+};
+
+/*
+ * Multi-query-row attention: encoder self-attention, causal prompt prefill,
+ * packed variable-length sequences, grouped-query attention.
+ *
+ *   out[b, i, h, :] = softmax_j(scale * q[b, i, h, :] . k[b, j, h / g, :]) v[b, j, h / g, :]
+ *   with g = heads_q / heads_kv and j over the keys sequence b uses.
+ *
+ * Sequence layout: with cu_seqlens_q == NULL, sequence b's query token t is
+ * at q + b * q_batch_stride + t * q_token_stride and every sequence has
+ * max_len_q queries (likewise keys with cu_seqlens_k / max_len_k).  With
+ * cu_seqlens_q != NULL (int32[batch + 1], device) sequences are packed: token
+ * t of sequence b is at q + (cu_seqlens_q[b] + t) * q_token_stride, the batch
+ * stride is ignored and the sequence has cu_seqlens_q[b+1] - cu_seqlens_q[b]
+ * queries (at most max_len_q).  seqused_k (int32[batch], device, optional)
+ * caps the keys sequence b uses.  A query with no visible key gets zeros.
+ *
+ * Replaces:
+ *   F.scaled_dot_product_attention   src/asrback/models/whisper.py:102-104
+ *       (encoder self-attention, whisper.py:108-110 via :124; causal prompt
+ *       prefix, whisper.py:235-237 with length set)
+ *   varlen_attn(..., seqused_k)      src/asrback/models/sensevoice.py:115-125
+ *   F.scaled_dot_product_attention   src/asrback/models/sensevoice.py:128-133
+ *   varlen_attn(..., window_size, enable_gqa)
+ *                                    src/asrback/models/qwen3_asr.py:156-166
+ *   F.scaled_dot_product_attention(..., enable_gqa=True)
+ *                                    src/asrback/models/qwen3_asr.py:176-180
+ */
+typedef struct asrattn_fwd_params {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* out;
+  int64_t q_batch_stride, q_token_stride, q_head_stride;
+  int64_t k_batch_stride, k_token_stride, k_head_stride;
+  int64_t v_batch_stride, v_token_stride, v_head_stride;
+  int64_t o_batch_stride, o_token_stride, o_head_stride;
+  const int32_t* cu_seqlens_q; /* int32[batch + 1] or NULL */
+  const int32_t* cu_seqlens_k; /* int32[batch + 1] or NULL */
+  const int32_t* seqused_k;    /* int32[batch] or NULL */
+  int32_t batch;
+  int32_t heads_q;
+  int32_t heads_kv; /* divides heads_q */
+  int32_t head_dim;
+  int32_t max_len_q;
+  int32_t max_len_k;
+  int32_t causal; /* enum asrattn_causal */
+  int32_t dtype;  /* enum asrattn_dtype */
+  float scale;    /* softmax scale; torch's default is 1 / sqrt(head_dim) */
+  int32_t flags;  /* 0, or ASRATTN_FWD_FORCE_VALU */
+} asrattn_fwd_params;
+
+int asrattn_fwd(const asrattn_fwd_params* params, void* stream);
+
+/*
+ * One query per sequence over a key/value cache (decoder step), split over
+ * the keys (split-K) and combined in a second pass.
+ *
+ *   out[b, h, :] = softmax_j(scale * q[b, h, :] . k[b, j, h / g, :]) v[b, j, h / g, :]
+ *   for j < n_b,  n_b = min(max_len_k, seqused_k[b])      (seqused_k given)
+ *                 n_b = min(max_len_k, positions[b] + 1)  (positions given)
+ *                 n_b = max_len_k                         (neither)
+ *
+ * k/v token t of sequence b, head h is at k + b*k_batch_stride +
+ * t*k_token_stride + h*k_head_stride: both cache layouts of the reference
+ * are plain strides, (batch, heads, length, head_dim) for Whisper and
+ * (batch, 1024, kv_heads, head_dim) for Qwen3-ASR.
+ *
+ * workspace: device memory of asrattn_decode_workspace_size(params) bytes
+ * (0 when a single split is used), owned by the caller; it must stay valid
+ * until the launch completes and must not be shared by concurrent calls.
+ *
+ * Replaces:
+ *   F.scaled_dot_product_attention with the (batch, 1, 1, length) position
+ *       mask                         src/asrback/models/whisper.py:235-237
+ *       (mask built at whisper.py:263-264)
+ *   F.scaled_dot_product_attention over the cross-attention cache
+ *                                    src/asrback/models/whisper.py:239-240
+ *   varlen_attn(..., seqused_k=positions + 1, num_splits, enable_gqa)
+ *                                    src/asrback/models/qwen3_asr.py:414-425
+ *   F.scaled_dot_product_attention with queries grouped per kv head
+ *                                    src/asrback/models/qwen3_asr.py:427-431
+ */
+typedef struct asrattn_decode_params {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* out;
+  int64_t q_batch_stride, q_head_stride;
+  int64_t k_batch_stride, k_token_stride, k_head_stride;
+  int64_t v_batch_stride, v_token_stride, v_head_stride;
+  int64_t o_batch_stride, o_head_stride;
+  const int32_t* seqused_k; /* int32[batch] or NULL */
+  const int64_t* positions; /* int64[batch] or NULL (ignored if seqused_k) */
+  int32_t batch;
+  int32_t heads_q;
+  int32_t heads_kv;
+  int32_t head_dim;
+  int32_t max_len_k;
+  int32_t num_splits; /* 0: chosen from batch, heads and max_len_k */
+  int32_t dtype;
+  float scale;
+} asrattn_decode_params;
+
+/* Bytes of workspace asrattn_decode needs for these parameters (pointers are
+ * not read).  Returns 0 for a single split, or (size_t)-1 on invalid params. */
+size_t asrattn_decode_workspace_size(const asrattn_decode_params* params);
+
+/* The split count asrattn_decode uses for these parameters. */
+int asrattn_decode_num_splits(const asrattn_decode_params* params);
+
+int asrattn_decode(const asrattn_decode_params* params, void* workspace,
+                   size_t workspace_bytes, void* stream);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* asrattn_last_error(void);
+
+/* ASRATTN_ABI_VERSION of the built library. */
+int asrattn_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ASRATTN_H */

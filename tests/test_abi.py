@@ -1,0 +1,142 @@
+"""CPU: the C ABI library loads, exports everything ``include/asrattn.h``
+declares, and the ctypes mirrors of its structs match the C layout.
+
+No kernel is launched here; argument checks that fail before any device work
+are exercised through the real library.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+import subprocess
+
+import pytest
+
+from conftest import ROOT
+
+HEADER = ROOT / "include" / "asrattn.h"
+
+
+def declared_functions() -> set[str]:
+    text = HEADER.read_text()
+    return set(re.findall(r"^\w[\w\s\*]*?\b(asrattn_\w+)\s*\(", text, flags=re.M))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    import torch  # noqa: F401  (the library binds to torch's HIP runtime)
+    from asrback_amd import _lib
+
+    if not _lib.LIBRARY.is_file():
+        from asrback_amd import build
+
+        build.build()
+    return _lib.load()
+
+
+def test_header_declares_expected_entry_points():
+    assert declared_functions() == {
+        "asrattn_fwd",
+        "asrattn_decode",
+        "asrattn_decode_workspace_size",
+        "asrattn_decode_num_splits",
+        "asrattn_last_error",
+        "asrattn_abi_version",
+    }
+
+
+def test_library_exports_every_declared_symbol(lib):
+    from asrback_amd import _lib
+
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    assert set(_lib.SIGNATURES) == declared_functions()
+
+
+def test_library_is_gfx950_and_binds_torch_runtime(lib):
+    from asrback_amd import _lib
+
+    maps = open("/proc/self/maps").read()
+    runtimes = {line.split()[-1] for line in maps.splitlines() if "libamdhip64" in line}
+    assert len(runtimes) == 1, runtimes  # one HIP runtime in the process: torch's
+    assert lib.asrattn_abi_version() == _lib.ABI_VERSION
+
+
+def _c_layout(struct: str, fields: list[str]) -> dict[str, int]:
+    """sizeof and offsetof as the C compiler lays the header's struct out."""
+    lines = [f'printf("sizeof %zu\\n", sizeof({struct}));']
+    lines += [f'printf("{f} %zu\\n", offsetof({struct}, {f}));' for f in fields]
+    source = (
+        "#include <stddef.h>\n#include <stdio.h>\n#include \"asrattn.h\"\n"
+        "int main(void) {\n" + "\n".join(lines) + "\nreturn 0; }\n"
+    )
+    import tempfile
+
+    with tempfile.TemporaryDirectory() as tmp:
+        src = f"{tmp}/layout.c"
+        exe = f"{tmp}/layout"
+        with open(src, "w") as f:
+            f.write(source)
+        subprocess.run(["gcc", "-std=c99", f"-I{ROOT / 'include'}", src, "-o", exe], check=True)
+        out = subprocess.run([exe], check=True, capture_output=True, text=True).stdout
+    return {k: int(v) for k, v in (line.split() for line in out.splitlines())}
+
+
+@pytest.mark.parametrize("name", ["FwdParams", "DecodeParams"])
+def test_ctypes_structs_match_c_layout(name):
+    from asrback_amd import _lib
+
+    cls = getattr(_lib, name)
+    struct = {"FwdParams": "asrattn_fwd_params", "DecodeParams": "asrattn_decode_params"}[name]
+    fields = [f for f, _ in cls._fields_]
+    layout = _c_layout(struct, fields)
+    assert layout.pop("sizeof") == ctypes.sizeof(cls)
+    for field in fields:
+        assert layout[field] == getattr(cls, field).offset, field
+
+
+def test_invalid_arguments_are_reported_not_fatal(lib):
+    from asrback_amd import _lib
+
+    p = _lib.DecodeParams()
+    p.batch, p.heads_q, p.heads_kv, p.head_dim, p.max_len_k = 1, 3, 2, 64, 10
+    p.dtype, p.scale = _lib.BF16, 0.125
+    status = lib.asrattn_decode(ctypes.byref(p), None, 0, None)
+    assert status == _lib.ERR_INVALID
+    assert b"heads_q" in lib.asrattn_last_error()
+
+    p.heads_q, p.heads_kv, p.head_dim = 2, 2, 96
+    assert lib.asrattn_decode(ctypes.byref(p), None, 0, None) == _lib.ERR_UNSUPPORTED
+    assert lib.asrattn_decode_workspace_size(ctypes.byref(p)) == ctypes.c_size_t(-1).value
+
+    f = _lib.FwdParams()
+    f.batch, f.heads_q, f.heads_kv, f.head_dim = 1, 1, 1, 64
+    f.max_len_q = f.max_len_k = 4
+    f.dtype, f.scale, f.causal = _lib.F32, 0.125, 7
+    assert lib.asrattn_fwd(ctypes.byref(f), None) == _lib.ERR_INVALID
+    assert b"causal" in lib.asrattn_last_error()
+    f.causal, f.scale = 0, float("nan")
+    assert lib.asrattn_fwd(ctypes.byref(f), None) == _lib.ERR_INVALID
+    f.scale = 0.125  # valid shape but NULL tensors
+    assert lib.asrattn_fwd(ctypes.byref(f), None) == _lib.ERR_INVALID
+    assert b"non-NULL" in lib.asrattn_last_error()
+
+
+def test_workspace_size_and_split_choice(lib):
+    from asrback_amd import _lib
+
+    p = _lib.DecodeParams()
+    # Whisper-small cross-attention: 16 rows x 12 heads over 1500 frames.
+    p.batch, p.heads_q, p.heads_kv, p.head_dim, p.max_len_k = 16, 12, 12, 64, 1500
+    p.dtype, p.scale = _lib.BF16, 0.125
+    splits = lib.asrattn_decode_num_splits(ctypes.byref(p))
+    assert splits > 1
+    assert lib.asrattn_decode_workspace_size(ctypes.byref(p)) == 16 * 12 * splits * (64 + 2) * 4
+    p.num_splits = 1
+    assert lib.asrattn_decode_workspace_size(ctypes.byref(p)) == 0
+    assert lib.asrattn_decode_num_splits(ctypes.byref(p)) == 1
+    # A missing workspace is an error, not a fault.
+    p.num_splits = 4
+    p.q = p.k = p.v = p.out = 16
+    assert lib.asrattn_decode(ctypes.byref(p), None, 0, None) == _lib.ERR_WORKSPACE

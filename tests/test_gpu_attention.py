@@ -1,0 +1,121 @@
+"""GPU parity of the attention kernels, called through the C ABI.
+
+Bar (stated per test): fp32 outputs within 1e-5 and bf16 outputs within 2e-2
+of a float32/float64 reference on the same (bf16-rounded) inputs, measured as
+max |out - ref| / max |ref|.  References: the committed golden vectors
+(float64 closed form) and, at the reference's configuration shapes, the CPU
+oracle (torch SDPA with the reference's masks).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import GOLDEN, max_rel_err
+from oracle import attention as oa
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float32: 1e-5, torch.bfloat16: 2e-2}
+DTYPES = [torch.float32, torch.bfloat16]
+
+
+@pytest.fixture(scope="module")
+def golden():
+    return np.load(GOLDEN / "attention_cases.npz")
+
+
+@pytest.fixture(scope="module")
+def ops():
+    from asrback_amd import attention
+
+    return attention
+
+
+def dev(x, dtype, device):
+    return torch.from_numpy(np.asarray(x)).to(device=device, dtype=dtype)
+
+
+def say(*args):
+    print(*args, flush=True)
+
+
+# --- golden vectors -----------------------------------------------------------
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("force_valu", [False, True])
+def test_encoder_golden(golden, ops, device, dtype, force_valu):
+    say("encoder golden", dtype, force_valu)
+    q, k, v = (dev(golden[f"enc_{n}"], dtype, device) for n in "qkv")
+    out = ops.flash(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), force_valu=force_valu)
+    assert max_rel_err(out.transpose(1, 2), golden["enc_out"]) < TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("force_valu", [False, True])
+def test_prefix_golden(golden, ops, device, dtype, force_valu):
+    say("prefix golden", dtype, force_valu)
+    q, k, v = (dev(golden[f"prefix_{n}"], dtype, device) for n in "qkv")
+    out = ops.flash(
+        q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), causal=1, force_valu=force_valu
+    )
+    assert max_rel_err(out.transpose(1, 2), golden["prefix_out"]) < TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_step_golden(golden, ops, device, dtype):
+    say("step golden", dtype)
+    q, k, v = (dev(golden[f"step_{n}"], dtype, device) for n in "qkv")
+    positions = torch.from_numpy(golden["step_positions"]).to(device)
+    out = ops.sdpa(q, k, v, ops.KeyPrefix(positions=positions))  # (B, 1, H, D)
+    assert max_rel_err(out.transpose(1, 2), golden["step_out"]) < TOL[dtype]
+    # The boolean mask the reference builds gives the same result.
+    mask = oa.whisper_step_mask(positions, k.shape[2])
+    out2 = ops.sdpa(q, k, v, mask)
+    assert max_rel_err(out2.transpose(1, 2), golden["step_out"]) < TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_cross_golden(golden, ops, device, dtype):
+    say("cross golden", dtype)
+    q, k, v = (dev(golden[f"cross_{n}"], dtype, device) for n in "qkv")
+    out = ops.sdpa(q, k, v)
+    assert max_rel_err(out.transpose(1, 2), golden["cross_out"]) < TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("force_valu", [False, True])
+def test_padded_golden(golden, ops, device, dtype, force_valu):
+    say("padded golden", dtype, force_valu)
+    q, k, v = (dev(golden[f"padded_{n}"], dtype, device) for n in "qkv")
+    lengths = torch.from_numpy(golden["padded_lengths"]).to(device)
+    out = ops.flash(
+        q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), seqused_k=lengths, force_valu=force_valu
+    )
+    assert max_rel_err(out.transpose(1, 2), golden["padded_out"]) < TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("force_valu", [False, True])
+def test_packed_gqa_golden(golden, ops, device, dtype, force_valu):
+    say("packed golden", dtype, force_valu)
+    q, k, v = (dev(golden[f"packed_{n}"], dtype, device) for n in "qkv")
+    starts = torch.from_numpy(golden["packed_starts"]).to(device)
+    longest = int(np.diff(golden["packed_starts"]).max())
+    out = ops.flash(
+        q, k, v, causal=2, cu_seqlens_q=starts, cu_seqlens_k=starts,
+        max_len_q=longest, max_len_k=longest, force_valu=force_valu,
+    )
+    assert max_rel_err(out, golden["packed_out"]) < TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_gqa_step_golden(golden, ops, device, dtype):
+    say("gqa step golden", dtype)
+    q, k, v = (dev(golden[f"gqa_step_{n}"], dtype, device) for n in "qkv")
+    used = torch.from_numpy(golden["gqa_step_used"]).to(device)
+    out = ops.decode(q, k, v, seqused_k=used)
+    assert max_rel_err(out, golden["gqa_step_out"]) < TOL[dtype]

@@ -1,0 +1,223 @@
+"""CPU: pins the oracle (``oracle/``) before any GPU result is compared with it.
+
+The oracle's attention calls go through torch's CPU SDPA; here they are
+checked against the independent float64 brute force (``oracle.brute``) and
+the committed golden vectors, and the brute force itself against special
+cases with known answers.  Mistakes these catch: a transposed mask, causal
+alignment off by one, the wrong kv head for a query head, a missing scale.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import GOLDEN, max_rel_err
+from oracle import attention as oa
+from oracle import brute
+
+
+@pytest.fixture(scope="module")
+def golden():
+    return np.load(GOLDEN / "attention_cases.npz")
+
+
+def t64(x):
+    return torch.from_numpy(np.asarray(x)).double()
+
+
+# --- the brute force against answers the mathematics fixes ---------------
+
+
+def test_brute_single_key_returns_its_value():
+    rng = np.random.default_rng(0)
+    q, k, v = rng.standard_normal((3, 1, 8))
+    out = brute.attention_rows(q, k, v, np.ones((1, 1), bool))
+    np.testing.assert_allclose(out, v, rtol=0, atol=1e-15)
+
+
+def test_brute_identical_keys_average_values():
+    rng = np.random.default_rng(1)
+    q = rng.standard_normal((2, 8))
+    k = np.repeat(rng.standard_normal((1, 8)), 5, axis=0)
+    v = rng.standard_normal((5, 8))
+    out = brute.attention_rows(q, k, v, np.ones((2, 5), bool))
+    np.testing.assert_allclose(out, np.repeat(v.mean(0, keepdims=True), 2, 0), atol=1e-14)
+
+
+def test_brute_two_keys_closed_form():
+    # softmax of two scores is a logistic function of their difference.
+    q = np.array([[1.0, 2.0, 0.0, 0.0]])
+    k = np.array([[1.0, 0.0, 0.0, 0.0], [0.0, 1.0, 0.0, 0.0]])
+    v = np.array([[1.0, 0.0, 0.0, 0.0], [0.0, 1.0, 0.0, 0.0]])
+    scale = 0.5
+    w1 = 1.0 / (1.0 + math.exp(-(2.0 - 1.0) * scale))
+    out = brute.attention_rows(q, k, v, np.ones((1, 2), bool), scale)
+    np.testing.assert_allclose(out[0, :2], [1 - w1, w1], atol=1e-15)
+
+
+def test_brute_masks():
+    top = brute.visible_mask(3, 3, causal="top_left")
+    assert top.tolist() == [[1, 0, 0], [1, 1, 0], [1, 1, 1]]
+    bottom = brute.visible_mask(2, 4, causal="bottom_right")
+    assert bottom.tolist() == [[1, 1, 1, 0], [1, 1, 1, 1]]
+    padded = brute.visible_mask(2, 4, n_keys=2)
+    assert padded.tolist() == [[1, 1, 0, 0], [1, 1, 0, 0]]
+
+
+# --- the oracle's call patterns against the golden vectors ---------------
+
+
+def test_oracle_encoder_matches_golden(golden):
+    q, k, v = (t64(golden[f"enc_{n}"]) for n in "qkv")
+    assert max_rel_err(oa.sdpa(q, k, v), golden["enc_out"]) < 1e-12
+
+
+def test_oracle_prefix_matches_golden(golden):
+    q, k, v = (t64(golden[f"prefix_{n}"]) for n in "qkv")
+    assert max_rel_err(oa.sdpa(q, k, v, is_causal=True), golden["prefix_out"]) < 1e-12
+
+
+def test_oracle_step_matches_golden(golden):
+    q, k, v = (t64(golden[f"step_{n}"]) for n in "qkv")
+    positions = torch.from_numpy(golden["step_positions"])
+    mask = oa.whisper_step_mask(positions, k.shape[2])
+    assert max_rel_err(oa.sdpa(q, k, v, attn_mask=mask), golden["step_out"]) < 1e-12
+
+
+def test_oracle_cross_matches_golden(golden):
+    q, k, v = (t64(golden[f"cross_{n}"]) for n in "qkv")
+    assert max_rel_err(oa.sdpa(q, k, v), golden["cross_out"]) < 1e-12
+
+
+def test_oracle_sensevoice_padding_matches_golden(golden):
+    q, k, v = (t64(golden[f"padded_{n}"]) for n in "qkv")  # (B, H, L, D)
+    lengths = torch.from_numpy(golden["padded_lengths"])
+    batch, heads, length, dim = q.shape
+    fused = torch.cat([t.transpose(1, 2).reshape(batch, length, heads * dim) for t in (q, k, v)], -1)
+    mask = oa.key_padding_mask(lengths, length)
+    out = oa.sensevoice_attention(fused, heads, mask)
+    ref = torch.from_numpy(golden["padded_out"]).transpose(1, 2).reshape(batch, length, heads * dim)
+    assert max_rel_err(out, ref) < 1e-12
+
+
+def test_oracle_packed_gqa_matches_golden(golden):
+    q, k, v = (t64(golden[f"packed_{n}"]) for n in "qkv")
+    starts = golden["packed_starts"]
+    segments = oa.Segments.from_lengths(np.diff(starts).tolist())
+    out = oa.qwen_attend(q, k, v, segments, causal=True)
+    assert max_rel_err(out, golden["packed_out"]) < 1e-12
+
+
+def test_oracle_gqa_step_matches_golden(golden):
+    q, k, v = (t64(golden[f"gqa_step_{n}"]) for n in "qkv")
+    used = torch.from_numpy(golden["gqa_step_used"]).long()
+    mask = oa.qwen_step_mask(used - 1, k.shape[1])
+    out = oa.qwen_step_attention(q, k, v, mask)
+    assert max_rel_err(out, golden["gqa_step_out"]) < 1e-12
+
+
+# --- invariants -------------------------------------------------------------
+
+
+def test_step_equals_last_row_of_causal_prefill():
+    g = torch.Generator().manual_seed(3)
+    q, k, v = (torch.randn(2, 3, 17, 64, generator=g, dtype=torch.float64) for _ in range(3))
+    full = oa.sdpa(q, k, v, is_causal=True)
+    for p in (0, 5, 16):
+        mask = oa.whisper_step_mask(torch.tensor([p, p]), 17)
+        step = oa.sdpa(q[:, :, p : p + 1], k, v, attn_mask=mask)
+        assert max_rel_err(step, full[:, :, p : p + 1]) < 1e-12
+
+
+def test_step_is_independent_of_cache_bucket():
+    g = torch.Generator().manual_seed(4)
+    q = torch.randn(3, 2, 1, 64, generator=g, dtype=torch.float64)
+    k, v = (torch.randn(3, 2, 448, 64, generator=g, dtype=torch.float64) for _ in range(2))
+    positions = torch.tensor([3, 40, 63])
+    outs = [
+        oa.sdpa(q, k[:, :, :L], v[:, :, :L], attn_mask=oa.whisper_step_mask(positions, L))
+        for L in (64, 128, 256, 448)
+    ]
+    for out in outs[1:]:
+        assert max_rel_err(out, outs[0]) < 1e-12
+
+
+def test_padded_batch_equals_per_sequence_runs():
+    g = torch.Generator().manual_seed(5)
+    lengths = torch.tensor([11, 4, 8])
+    fused = torch.randn(3, 11, 3 * 256, generator=g, dtype=torch.float64)
+    out = oa.sensevoice_attention(fused, 2, oa.key_padding_mask(lengths, 11))
+    for b, n in enumerate(lengths.tolist()):
+        alone = oa.sensevoice_attention(fused[b : b + 1, :n], 2, None)
+        assert max_rel_err(out[b, :n], alone[0]) < 1e-12
+
+
+def test_gqa_equals_repeated_kv_heads():
+    g = torch.Generator().manual_seed(6)
+    q = torch.randn(2, 4, 128, generator=g, dtype=torch.float64)
+    k, v = (torch.randn(2, 30, 2, 128, generator=g, dtype=torch.float64) for _ in range(2))
+    mask = oa.qwen_step_mask(torch.tensor([10, 29]), 30)
+    grouped = oa.qwen_step_attention(q, k, v, mask)
+    # MHA with kv head h // 2 repeated for query head h.
+    k_rep = k.repeat_interleave(2, dim=2).transpose(1, 2)
+    v_rep = v.repeat_interleave(2, dim=2).transpose(1, 2)
+    mha = oa.sdpa(q[:, :, None], k_rep, v_rep, attn_mask=mask)[:, :, 0]
+    assert max_rel_err(grouped, mha) < 1e-12
+
+
+def test_rope_identity_at_position_zero_and_norm_preserving():
+    cos, sin = oa.rope_tables(1e6, 128, 1024, torch.float64)
+    x = torch.randn(5, 16, 128, dtype=torch.float64)
+    assert torch.equal(oa.rotate(x, cos[0].expand(5, 128), sin[0].expand(5, 128)), x)
+    positions = torch.tensor([1, 7, 100, 555, 1023])
+    rotated = oa.rotate(x, cos[positions], sin[positions])
+    # The angles are float32 (as the reference computes them): cos^2 + sin^2
+    # is 1 to about 1e-8.
+    torch.testing.assert_close(rotated.norm(dim=-1), x.norm(dim=-1), rtol=1e-7, atol=0)
+
+
+def test_rope_scores_depend_only_on_position_difference():
+    cos, sin = oa.rope_tables(1e6, 128, 1024, torch.float64)
+    q = torch.randn(1, 1, 128, dtype=torch.float64)
+    k = torch.randn(1, 1, 128, dtype=torch.float64)
+
+    def score(m, n):
+        qm = oa.rotate(q, cos[m : m + 1], sin[m : m + 1])
+        kn = oa.rotate(k, cos[n : n + 1], sin[n : n + 1])
+        return float((qm * kn).sum())
+
+    assert abs(score(10, 3) - score(507, 500)) < 1e-4  # float32 angles
+    assert abs(score(0, 0) - float((q * k).sum())) < 1e-12
+
+
+def test_rms_norm_formula():
+    x = torch.randn(4, 16, 128, dtype=torch.float64)
+    w = torch.randn(128, dtype=torch.float64)
+    ref = x / torch.sqrt((x * x).mean(-1, keepdim=True) + 1e-6) * w
+    torch.testing.assert_close(oa.rms_norm(x, w, 1e-6), ref, rtol=1e-12, atol=1e-12)
+
+
+def test_fsmn_matches_explicit_loop():
+    g = torch.Generator().manual_seed(7)
+    value = torch.randn(2, 9, 4, generator=g, dtype=torch.float64)
+    weight = torch.randn(4, 1, 11, generator=g, dtype=torch.float64)
+    mask = oa.key_padding_mask(torch.tensor([9, 6]), 9)
+    out = oa.fsmn_memory(value, mask, weight, 11)
+    keep = mask[..., None].double()
+    masked = value * keep
+    ref = torch.zeros_like(value)
+    for b in range(2):
+        for t in range(9):
+            for c in range(4):
+                acc = 0.0
+                for i in range(11):
+                    s = t + i - 5  # left padding (11 - 1) // 2 = 5
+                    if 0 <= s < 9:
+                        acc += float(weight[c, 0, i]) * float(masked[b, s, c])
+                ref[b, t, c] = acc
+    ref = (ref + masked) * keep
+    torch.testing.assert_close(out, ref, rtol=1e-12, atol=1e-12)
