@@ -1,0 +1,450 @@
+#!/usr/bin/env python3
+"""Throughput of the asrback attention hot path on one MI355X.
+
+Prints one JSON line.  The headline workload is SenseVoiceSmall's SAN-M
+encoder self-attention in bf16 (4 heads x 128, 70 layers, batch 32 with
+ragged lengths of 104-504 frames and key padding): a step is the attention of
+all 70 layers over one batch, q/k/v read in place from per-layer fused
+projection buffers (token stride 1536) already resident in HBM, the 70
+launches replayed from one hipGraph.  ``value`` is algorithmic TFLOP/s:
+sum_b 4 * L_b^2 * 512 per layer over valid queries x valid keys.
+
+Decode is reported beside it (``decode``): Qwen3-ASR-1.7B's GQA decoder step
+(28 layers, 16 query / 8 kv heads x 128, batch 64, prompts of 400-430 tokens,
+a (28, 64, 1024, 8, 128) cache, 128 steps) and Whisper-small's decoder step
+(12 layers, 12 heads x 64, batch 16, self keys 1-224, cross-attention over
+1500 frames), in algorithmic HBM GB/s (K and V of the keys each row uses,
+plus q and o).  ``secondary`` adds Whisper large-v3-turbo's encoder attention
+(20 heads x 64, 1500 frames, batch 16, 32 layers).
+
+``cpu_baseline`` times the CPU restatement of the reference's attention
+(torch SDPA with the key-padding mask, float32, the reference's CPU path) on
+a bounded sample of the headline workload on this machine's host cores.
+
+    python bench.py [--steps K] [--warmup W] [--no-cpu-baseline] [--only NAME]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0  # MI355X HBM3E
+METRIC = "attn TFLOP/s (encoder) & HBM GB/s (decode step), % of MI355X roofline"
+
+
+def log(*args) -> None:
+    print(*args, file=sys.stderr, flush=True)
+
+
+class Workload:
+    """A step of attention launches over inputs resident in HBM."""
+
+    name: str
+    unit: str
+    bound: str
+    kernel: str  # the dominant kernel (rocprof name prefix)
+    launches: int  # launches of ``kernel`` per step
+    work_per_step: float  # flop or bytes
+
+    def run(self) -> None:
+        raise NotImplementedError
+
+    def config(self) -> dict:
+        raise NotImplementedError
+
+
+class SenseVoiceEncoder(Workload):
+    """SAN-M encoder self-attention (sensevoice.py:94-135): fused qkv
+    ``(B, L, 1536)`` per layer, key padding by ``lengths = T + 4``."""
+
+    name = "sensevoice-small-encoder-attention"
+    unit = "TFLOP/s"
+    bound = "mfma"
+    kernel = "fwd_mfma_kernel"
+
+    def __init__(self, torch, attention, seed: int = 1) -> None:
+        rng = np.random.default_rng(seed)
+        self.batch, self.heads, self.head_dim, self.layers = 32, 4, 128, 70
+        frames = rng.integers(100, 501, size=self.batch)  # LFR frames, U{100..500}
+        self.lengths_host = (frames + 4).astype(np.int32)  # four query embeddings in front
+        self.length = int(self.lengths_host.max())
+        width = self.heads * self.head_dim
+        g = torch.Generator(device="cuda").manual_seed(seed)
+        self.qkv = [
+            torch.randn((self.batch, self.length, 3 * width), generator=g, device="cuda", dtype=torch.bfloat16)
+            for _ in range(self.layers)
+        ]
+        self.lengths = torch.from_numpy(self.lengths_host).cuda()
+        self.out = torch.empty((self.batch, self.length, self.heads, self.head_dim), device="cuda", dtype=torch.bfloat16)
+        self.attention = attention
+        self.launches = self.layers
+        per_layer = float(sum(4 * int(n) ** 2 * width for n in self.lengths_host))
+        self.work_per_step = per_layer * self.layers
+
+    def views(self, layer: int):
+        q, k, v = self.qkv[layer].split(self.heads * self.head_dim, dim=-1)
+        shape = (self.batch, self.length, self.heads, self.head_dim)
+        return q.view(shape), k.view(shape), v.view(shape)
+
+    def run(self) -> None:
+        for layer in range(self.layers):
+            q, k, v = self.views(layer)
+            self.attention.flash(q, k, v, seqused_k=self.lengths, out=self.out)
+
+    def config(self) -> dict:
+        return {
+            "workload": self.name,
+            "batch": self.batch,
+            "heads": self.heads,
+            "head_dim": self.head_dim,
+            "layers": self.layers,
+            "frames": "U{100..500} + 4 queries, key padding",
+            "lengths_mean": float(self.lengths_host.mean()),
+            "max_length": self.length,
+        }
+
+
+class WhisperTurboEncoder(Workload):
+    """Whisper large-v3-turbo encoder self-attention (whisper.py:102-110):
+    q/k/v ``(16, 20, 1500, 64)`` views of ``(16, 1500, 1280)`` projections."""
+
+    name = "whisper-large-v3-turbo-encoder-attention"
+    unit = "TFLOP/s"
+    bound = "mfma"
+    kernel = "fwd_mfma_kernel"
+
+    def __init__(self, torch, attention, seed: int = 2) -> None:
+        self.batch, self.heads, self.head_dim, self.layers, self.length = 16, 20, 64, 32, 1500
+        width = self.heads * self.head_dim
+        g = torch.Generator(device="cuda").manual_seed(seed)
+        self.qkv = [
+            torch.randn((self.batch, self.length, 3 * width), generator=g, device="cuda", dtype=torch.bfloat16)
+            for _ in range(self.layers)
+        ]
+        self.out = torch.empty((self.batch, self.length, self.heads, self.head_dim), device="cuda", dtype=torch.bfloat16)
+        self.attention = attention
+        self.launches = self.layers
+        self.work_per_step = 4.0 * self.length**2 * width * self.batch * self.layers
+
+    def run(self) -> None:
+        width = self.heads * self.head_dim
+        shape = (self.batch, self.length, self.heads, self.head_dim)
+        for layer in range(self.layers):
+            q, k, v = (t.view(shape) for t in self.qkv[layer].split(width, dim=-1))
+            self.attention.flash(q, k, v, out=self.out)
+
+    def config(self) -> dict:
+        return {"workload": self.name, "batch": self.batch, "heads": self.heads, "head_dim": self.head_dim,
+                "layers": self.layers, "frames": self.length}
+
+
+class Qwen3Decode(Workload):
+    """Qwen3-ASR-1.7B GQA decoder step (qwen3_asr.py:392-432): q ``(64, 16,
+    128)`` over the ``(28, 64, 1024, 8, 128)`` cache, ``seqused_k =
+    position + 1``; each step advances every row by one position, 128 steps
+    from prompts of 390 + U{10..40} tokens."""
+
+    name = "qwen3-asr-1.7b-decode-attention"
+    unit = "GB/s"
+    bound = "hbm"
+    kernel = "decode_split_kernel"
+
+    def __init__(self, torch, attention, seed: int = 3, steps: int = 128) -> None:
+        rng = np.random.default_rng(seed)
+        self.torch = torch
+        self.batch, self.heads_q, self.heads_kv, self.head_dim, self.layers = 64, 16, 8, 128, 28
+        self.cache_length, self.steps = 1024, steps
+        self.prompts = (390 + rng.integers(10, 41, size=self.batch)).astype(np.int64)
+        shape = (self.layers, self.batch, self.cache_length, self.heads_kv, self.head_dim)
+        g = torch.Generator(device="cuda").manual_seed(seed)
+        self.keys = torch.randn(shape, generator=g, device="cuda", dtype=torch.bfloat16)
+        self.values = torch.randn(shape, generator=g, device="cuda", dtype=torch.bfloat16)
+        self.q = torch.randn((self.layers, self.batch, self.heads_q, self.head_dim), generator=g, device="cuda",
+                             dtype=torch.bfloat16)
+        self.out = torch.empty((self.batch, self.heads_q, self.head_dim), device="cuda", dtype=torch.bfloat16)
+        self.start = torch.from_numpy(self.prompts - 1).cuda()  # position of the last prompt token
+        self.positions = self.start.clone()
+        self.used = torch.empty(self.batch, dtype=torch.int32, device="cuda")
+        self.attention = attention
+        self.launches = self.layers
+        # Step t attends P_b + t + 1 keys (the new token's key included).
+        row_bytes = 2 * self.heads_kv * self.head_dim * 2  # K and V, bf16
+        qo_bytes = 2 * self.heads_q * self.head_dim * 2
+        self.step_bytes = [
+            self.layers * float(sum(row_bytes * (int(p) + t + 1) + qo_bytes for p in self.prompts))
+            for t in range(self.steps)
+        ]
+        self.work_per_step = float(np.mean(self.step_bytes))
+
+    def reset(self) -> None:
+        self.positions.copy_(self.start)
+
+    def run(self) -> None:
+        self.positions.add_(1)
+        self.used.copy_(self.positions + 1)  # seqused_k = position + 1 (int32)
+        for layer in range(self.layers):
+            self.attention.decode(self.q[layer], self.keys[layer], self.values[layer], seqused_k=self.used,
+                                  out=self.out)
+
+    def config(self) -> dict:
+        return {"workload": self.name, "batch": self.batch, "heads_q": self.heads_q, "heads_kv": self.heads_kv,
+                "head_dim": self.head_dim, "layers": self.layers, "cache": list(self.keys.shape[1:]),
+                "prompt_tokens": "390 + U{10..40}", "steps": self.steps}
+
+
+class WhisperSmallDecoderStep(Workload):
+    """Whisper-small decoder step (whisper.py:212-277): per layer, self-attention
+    over the ``(16, 12, 256, 64)`` KV bucket view (keys 0..position, positions
+    U{0..223}) and cross-attention over ``(16, 12, 1500, 64)``."""
+
+    name = "whisper-small-decoder-step-attention"
+    unit = "GB/s"
+    bound = "hbm"
+    kernel = "decode_split_kernel"
+
+    def __init__(self, torch, attention, seed: int = 4) -> None:
+        rng = np.random.default_rng(seed)
+        self.batch, self.heads, self.head_dim, self.layers = 16, 12, 64, 12
+        self.positions_host = rng.integers(0, 224, size=self.batch).astype(np.int64)
+        g = torch.Generator(device="cuda").manual_seed(seed)
+        self.self_keys = torch.randn((self.layers, self.batch, self.heads, 448, self.head_dim), generator=g,
+                                     device="cuda", dtype=torch.bfloat16)
+        self.self_values = torch.randn_like(self.self_keys)
+        self.cross_keys = torch.randn((self.layers, self.batch, self.heads, 1500, self.head_dim), generator=g,
+                                      device="cuda", dtype=torch.bfloat16)
+        self.cross_values = torch.randn_like(self.cross_keys)
+        self.q = torch.randn((self.layers, 2, self.batch, self.heads, self.head_dim), generator=g, device="cuda",
+                             dtype=torch.bfloat16)
+        self.out = torch.empty((self.batch, self.heads, self.head_dim), device="cuda", dtype=torch.bfloat16)
+        self.positions = torch.from_numpy(self.positions_host).cuda()
+        self.attention = attention
+        self.launches = 2 * self.layers
+        row = self.heads * self.head_dim * 2
+        qo = 2 * row
+        self_bytes = sum(2 * row * (int(p) + 1) + qo for p in self.positions_host)
+        cross_bytes = self.batch * (2 * row * 1500 + qo)
+        self.work_per_step = float(self.layers * (self_bytes + cross_bytes))
+
+    def run(self) -> None:
+        bucket = 256
+        for layer in range(self.layers):
+            k = self.self_keys[layer, :, :, :bucket].transpose(1, 2)
+            v = self.self_values[layer, :, :, :bucket].transpose(1, 2)
+            self.attention.decode(self.q[layer, 0], k, v, positions=self.positions, out=self.out)
+            self.attention.decode(self.q[layer, 1], self.cross_keys[layer].transpose(1, 2),
+                                  self.cross_values[layer].transpose(1, 2), out=self.out)
+
+    def config(self) -> dict:
+        return {"workload": self.name, "batch": self.batch, "heads": self.heads, "head_dim": self.head_dim,
+                "layers": self.layers, "self_keys": "U{1..224} in a 256 bucket", "cross_frames": 1500}
+
+
+def time_graph(torch, workload: Workload, steps: int, warmup: int, reset=None) -> float:
+    """Milliseconds per step: the step captured once as a hipGraph, ``warmup``
+    untimed replays, then ``steps`` replays between HIP events on the
+    launching stream, with a device synchronization on both sides."""
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for _ in range(2):
+            workload.run()
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        workload.run()
+    if reset is not None:
+        reset()
+    for _ in range(warmup):
+        graph.replay()
+    if reset is not None:
+        reset()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        graph.replay()
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / steps
+
+
+def roofline(workload: Workload, ms_per_step: float, work_per_step: float) -> dict:
+    seconds = ms_per_step / 1e3
+    if workload.unit == "TFLOP/s":
+        achieved = work_per_step / seconds / 1e12
+        peak = PEAK_BF16_TFLOPS
+    else:
+        achieved = work_per_step / seconds / 1e9
+        peak = PEAK_HBM_GBS
+    return {
+        "bound": workload.bound,
+        "achieved": round(achieved, 2),
+        "peak": peak,
+        "unit": workload.unit,
+        "frac": round(achieved / peak, 4),
+        "traffic": None,
+        "kernel": workload.kernel,
+        "launches_per_step": workload.launches,
+        "avg_launch_us": round(ms_per_step * 1e3 / workload.launches, 2),
+    }
+
+
+def measure(torch, workload: Workload, steps: int, warmup: int) -> dict:
+    if isinstance(workload, Qwen3Decode):
+        # The 128-step decode: the timed steps advance the positions.
+        steps = min(steps, workload.steps)
+        ms = time_graph(torch, workload, steps, min(warmup, workload.steps), reset=workload.reset)
+        work = float(np.mean(workload.step_bytes[:steps]))
+    else:
+        ms = time_graph(torch, workload, steps, warmup)
+        work = workload.work_per_step
+    seconds = ms / 1e3
+    value = work / seconds / (1e12 if workload.unit == "TFLOP/s" else 1e9)
+    return {
+        "workload": workload.name,
+        "value": round(value, 2),
+        "unit": workload.unit,
+        "ms_per_step": round(ms, 4),
+        "roofline": roofline(workload, ms, work),
+        "config": workload.config(),
+    }
+
+
+def cpu_baseline(budget_s: float = 12.0) -> dict:
+    """The reference's CPU path (oracle: torch SDPA with the key-padding mask,
+    float32) on the headline batch, as many layers as fit in ``budget_s``."""
+    import torch
+
+    from oracle import attention as oa
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    rng = np.random.default_rng(1)
+    frames = rng.integers(100, 501, size=32)
+    lengths = torch.from_numpy((frames + 4).astype(np.int64))
+    length = int(lengths.max())
+    g = torch.Generator().manual_seed(1)
+    qkv = torch.randn((32, length, 3 * 512), generator=g)
+    mask = oa.key_padding_mask(lengths, length)
+    per_layer = float(sum(4 * int(n) ** 2 * 512 for n in lengths))
+    oa.sensevoice_attention(qkv, 4, mask)  # warm-up
+    layers = 0
+    start = time.perf_counter()
+    while True:
+        oa.sensevoice_attention(qkv, 4, mask)
+        layers += 1
+        elapsed = time.perf_counter() - start
+        if elapsed > budget_s or layers >= 70:
+            break
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": round(per_layer * layers / elapsed / 1e12, 4),
+        "unit": "TFLOP/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"{layers} of the 70 layers of the headline batch (B=32, lengths {int(lengths.min())}-"
+        f"{length}), float32, torch CPU SDPA with key-padding mask; {model}",
+        "seconds": round(elapsed, 2),
+    }
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=20)
+    parser.add_argument("--warmup", type=int, default=5)
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--only", choices=["sensevoice", "turbo", "qwen3", "whisper-small"], default=None,
+                        help="measure one workload only (for profiling)")
+    args = parser.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(
+            "bench.py measures one GPU: the attention path runs one model per process on one device "
+            f"(asked for --gpus {args.gpus}, WORLD_SIZE {world}); run it with --gpus 1.",
+            file=sys.stderr,
+        )
+        return 2
+
+    import torch
+
+    from asrback_amd import attention
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    torch.cuda.set_device(0)
+    selected = {
+        "sensevoice": SenseVoiceEncoder,
+        "turbo": WhisperTurboEncoder,
+        "qwen3": Qwen3Decode,
+        "whisper-small": WhisperSmallDecoderStep,
+    }
+    if args.only:
+        workload = selected[args.only](torch, attention)
+        result = measure(torch, workload, args.steps, args.warmup)
+        log(json.dumps(result))
+        print(json.dumps(result))
+        return 0
+
+    log("bench: sensevoice encoder attention")
+    head = measure(torch, SenseVoiceEncoder(torch, attention), args.steps, args.warmup)
+    torch.cuda.empty_cache()
+    decode = []
+    for cls in (Qwen3Decode, WhisperSmallDecoderStep):
+        log(f"bench: {cls.name}")
+        decode.append(measure(torch, cls(torch, attention), args.steps, args.warmup))
+        torch.cuda.empty_cache()
+    log("bench: whisper turbo encoder attention")
+    secondary = [measure(torch, WhisperTurboEncoder(torch, attention), args.steps, args.warmup)]
+    torch.cuda.empty_cache()
+    baseline = None
+    if not args.no_cpu_baseline:
+        log("bench: cpu baseline")
+        baseline = cpu_baseline()
+
+    line = {
+        "metric": METRIC,
+        "value": head["value"],
+        "unit": head["unit"],
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) q/k/v and caches, resident in HBM)",
+        "config": head["config"],
+        "roofline": head["roofline"],
+        "cpu_baseline": baseline,
+        "decode": decode,
+        "secondary": secondary,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
