@@ -261,6 +261,7 @@ def decode(
     num_splits: int = 0,
     scale: float | None = None,
     out: Tensor | None = None,
+    workspace: Tensor | None = None,
 ) -> Tensor:
     """One query per sequence over a cache (``asrattn_decode``).
 
@@ -269,7 +270,7 @@ def decode(
     ``cache.transpose(1, 2)`` for a ``(batch, heads, length, head_dim)``
     cache).  Sequence ``b`` uses keys ``0 .. n_b - 1`` with ``n_b =
     seqused_k[b]`` (int32), ``positions[b] + 1`` (int64) or ``length``.
-    Returns ``(batch, heads_q, head_dim)``.
+    ``workspace`` defaults to the device's shared one.  Returns ``(batch, heads_q, head_dim)``.
     """
     if q.dim() != 3 or k.dim() != 4 or v.shape != k.shape:
         raise ValueError(
@@ -302,16 +303,36 @@ def decode(
     need = lib.asrattn_decode_workspace_size(ctypes.byref(params))
     if need == ctypes.c_size_t(-1).value:
         _lib.check(lib.asrattn_decode(ctypes.byref(params), None, 0, _stream(device)), "asrattn_decode")
-    workspace = None
-    if need:
-        workspace = torch.empty(need, dtype=torch.uint8, device=device)
+    if workspace is None and need:
+        workspace = decode_workspace(need, device)
+    size = 0 if workspace is None else workspace.numel() * workspace.element_size()
     _lib.check(
-        lib.asrattn_decode(
-            ctypes.byref(params), _ptr(workspace), need, _stream(device)
-        ),
+        lib.asrattn_decode(ctypes.byref(params), _ptr(workspace), size, _stream(device)),
         "asrattn_decode",
     )
     return out
+
+
+# Decode workspaces per device: one buffer serves every call on the device
+# (calls on one device run in stream order); grown buffers are kept alive
+# because graphs captured earlier still hold their addresses.
+_workspaces: dict[torch.device, list[Tensor]] = {}
+
+
+def decode_workspace(nbytes: int, device: torch.device) -> Tensor:
+    """A decode workspace of at least ``nbytes`` on ``device``, shared by
+    every :func:`decode` on that device (calls on one device must not run
+    concurrently on different streams)."""
+    device = torch.device(device)
+    if device.index is None:
+        device = torch.device(device.type, torch.cuda.current_device())
+    held = _workspaces.setdefault(device, [])
+    if held and held[-1].numel() >= nbytes:
+        return held[-1]
+    size = max(nbytes, 2 * held[-1].numel() if held else 1 << 20)
+    buffer = torch.empty(size, dtype=torch.uint8, device=device)
+    held.append(buffer)
+    return buffer
 
 
 def sdpa(

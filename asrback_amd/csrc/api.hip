@@ -60,11 +60,13 @@ int from_hip(hipError_t err, const char* what) {
 
 int decode_splits(const asrattn_decode_params& p) {
   if (p.num_splits > 0) return p.num_splits;
-  // About four workgroups per CU (256 CUs) in flight, but at least 128 keys
-  // per split so a split streams whole load batches.
+  // One workgroup per (sequence, kv head) once there are enough of them to
+  // spread over the 256 CUs; fewer get their keys split, at least 256 keys
+  // per split.
   const long long pairs = (long long)p.batch * p.heads_kv;
-  long long s = (1024 + pairs - 1) / pairs;
-  const long long by_len = (p.max_len_k + 127) / 128;
+  if (pairs >= 128) return 1;
+  long long s = (256 + pairs - 1) / pairs;
+  const long long by_len = (p.max_len_k + 255) / 256;
   if (s > by_len) s = by_len;
   if (s > 64) s = 64;
   if (s < 1) s = 1;
@@ -88,9 +90,32 @@ int check_decode(const asrattn_decode_params* p) {
   return ASRATTN_OK;
 }
 
+// Workspace layout: partial outputs, then (max, sum) pairs, each section
+// 256-byte aligned.
+struct DecodeWorkspace {
+  size_t partials, stats, total;
+};
+
+size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+DecodeWorkspace decode_workspace(const asrattn_decode_params& p, int splits) {
+  DecodeWorkspace w{0, 0, 0};
+  if (splits == 1) return w;
+  const size_t rows = (size_t)p.batch * p.heads_q * splits;
+  w.partials = 0;
+  w.stats = align256(rows * (size_t)p.head_dim * sizeof(float));
+  w.total = w.stats + align256(rows * 2 * sizeof(float));
+  return w;
+}
+
 }  // namespace
 
 extern "C" {
+
+size_t asrattn_decode_workspace_size(const asrattn_decode_params* params) {
+  if (check_decode(params) != ASRATTN_OK) return (size_t)-1;
+  return decode_workspace(*params, decode_splits(*params)).total;
+}
 
 const char* asrattn_last_error(void) { return g_last_error.c_str(); }
 
@@ -130,14 +155,7 @@ int asrattn_decode_num_splits(const asrattn_decode_params* params) {
   return decode_splits(*params);
 }
 
-size_t asrattn_decode_workspace_size(const asrattn_decode_params* params) {
-  if (check_decode(params) != ASRATTN_OK) return (size_t)-1;
-  const asrattn_decode_params& p = *params;
-  const int s = decode_splits(p);
-  if (s == 1) return 0;
-  const size_t rows = (size_t)p.batch * p.heads_q * s;
-  return rows * (size_t)p.head_dim * sizeof(float) + rows * 2 * sizeof(float);
-}
+
 
 int asrattn_decode(const asrattn_decode_params* params, void* workspace, size_t workspace_bytes, void* stream) {
   int rc = check_decode(params);
@@ -152,19 +170,21 @@ int asrattn_decode(const asrattn_decode_params* params, void* workspace, size_t 
     return fail(ASRATTN_ERR_INVALID,
                 "q, k and v need 16-byte aligned pointers and strides that are multiples of 16 bytes");
   const int s = decode_splits(p);
-  const size_t need = asrattn_decode_workspace_size(params);
+  const DecodeWorkspace w = decode_workspace(p, s);
   float* ws_o = nullptr;
   float* ws_ml = nullptr;
   if (s > 1) {
-    if (workspace == nullptr || workspace_bytes < need)
-      return fail(ASRATTN_ERR_WORKSPACE, "decode needs %zu workspace bytes, got %zu", need,
+    if (workspace == nullptr || workspace_bytes < w.total)
+      return fail(ASRATTN_ERR_WORKSPACE, "decode needs %zu workspace bytes, got %zu", w.total,
                   workspace == nullptr ? (size_t)0 : workspace_bytes);
-    if ((reinterpret_cast<uintptr_t>(workspace) & 15u) != 0)
-      return fail(ASRATTN_ERR_WORKSPACE, "workspace must be 16-byte aligned");
-    ws_o = static_cast<float*>(workspace);
-    ws_ml = ws_o + (size_t)p.batch * p.heads_q * s * p.head_dim;
+    if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
+      return fail(ASRATTN_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+    char* base = static_cast<char*>(workspace);
+    ws_o = reinterpret_cast<float*>(base + w.partials);
+    ws_ml = reinterpret_cast<float*>(base + w.stats);
   }
-  return from_hip(asrattn::launch_decode(p, s, ws_o, ws_ml, static_cast<hipStream_t>(stream)), "asrattn_decode");
+  return from_hip(asrattn::launch_decode(p, s, ws_o, ws_ml, static_cast<hipStream_t>(stream)),
+                  "asrattn_decode");
 }
 
 }  // extern "C"

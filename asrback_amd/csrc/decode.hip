@@ -2,18 +2,22 @@
 //
 // The step is bound by HBM: every key and value of a sequence is read once
 // and used for one (or, with grouped-query attention, g) dot products.  The
-// kernel therefore streams K and V with 16-byte loads, many in flight per
-// lane, and keeps all arithmetic in registers:
+// kernel therefore streams K and V with 16-byte loads, keeps a second batch
+// of loads in flight while it consumes the first, and does all arithmetic in
+// registers:
 //
 //   * A key row (head_dim elements) is covered by LPK lanes, 16 bytes each;
 //     a wave loads 64 / LPK key rows per instruction, so every load touches
 //     whole rows.  Each group of LPK lanes runs its own online softmax over
 //     the keys it reads (a "stream"); the g query heads sharing the kv head
 //     ride along on the same loads.
-//   * The keys of a sequence are split over gridDim.x workgroups (split-K);
-//     the streams of a workgroup merge in LDS and each split writes an
-//     unnormalized partial (o, max, sum) to the workspace, which the combine
-//     pass folds into the output.  A single split writes the output directly.
+//   * A workgroup of W waves covers one (sequence, kv head) -- or, for small
+//     batches, one of `splits` key ranges of it.  Its streams merge first
+//     inside each wave (butterfly shuffles) and then across waves in LDS.
+//     With enough (sequence, kv head) pairs to fill the GPU there is one
+//     split and the workgroup writes the output; otherwise each split writes
+//     an unnormalized partial (o, max, sum) and a small combine kernel folds
+//     them.  No workgroup waits on another.
 //   * Sequence lengths are read from device memory (seqused_k or
 //     positions + 1), and splits past a sequence's end write an empty
 //     partial, so the grid depends only on shapes and the launch can be
@@ -29,30 +33,23 @@ namespace {
 
 struct DecodeArgs {
   asrattn_decode_params p;
-  float* ws_o;
-  float* ws_ml;
+  float* ws_o;   // [batch][heads_q][splits][head_dim]
+  float* ws_ml;  // [batch][heads_q][splits][2]
   int splits;
   float c;  // scale * log2(e)
 };
 
-constexpr int kDecodeThreads = 256;  // four waves per workgroup
-
-template <typename T, int HD>
+template <typename T, int HD, int W>
 struct DecodeShape {
   static constexpr int kEPL = Elem<T>::kPerVec;   // elements per lane per load
   static constexpr int kLPK = HD / kEPL;          // lanes per key row
-  static constexpr int kKPW = 64 / kLPK;          // key rows per wave load
-  static constexpr int kThreads = kDecodeThreads;
-  static constexpr int kWaves = kThreads / 64;
-  static constexpr int kStreams = kWaves * kKPW;  // softmax streams per workgroup
-  static constexpr int kUnroll = 8;               // keys per stream per iteration
+  static constexpr int kKPW = 64 / kLPK;          // key rows per wave load (streams per wave)
+  static constexpr int kThreads = 64 * W;
+  static constexpr int kStreams = W * kKPW;       // softmax streams per workgroup
+  static constexpr int kUnroll = 4;               // keys per stream per load batch
+  static constexpr int kStep = kStreams * kUnroll;  // keys per load batch
   static_assert(kLPK >= 1 && kLPK <= 64 && (64 % kLPK) == 0, "head_dim/lane mapping");
 };
-
-template <typename T>
-__device__ __forceinline__ uint4 load_vec(const T* p) {
-  return *reinterpret_cast<const uint4*>(p);
-}
 
 template <typename T>
 __device__ __forceinline__ void unpack(const uint4& r, float* out);
@@ -71,10 +68,96 @@ __device__ __forceinline__ void unpack<bf16_raw>(const uint4& r, float* out) {
   out[6] = bf16_lo(r.w); out[7] = bf16_hi(r.w);
 }
 
-template <typename T, int HD, int G>
-__global__ __launch_bounds__(kDecodeThreads) void decode_split_kernel(const DecodeArgs a) {
-  using S = DecodeShape<T, HD>;
-  constexpr int EPL = S::kEPL, LPK = S::kLPK, NS = S::kStreams, U = S::kUnroll;
+// Online-softmax state of one stream for the G query heads of a kv head.
+template <typename T, int HD, int G, int W>
+struct Stream {
+  using S = DecodeShape<T, HD, W>;
+  static constexpr int EPL = S::kEPL;
+  float q[G][EPL];
+  float m[G], l[G], o[G][EPL];
+
+  __device__ __forceinline__ void init() {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      m[g] = kNegInf;
+      l[g] = 0.f;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) o[g][e] = 0.f;
+    }
+  }
+
+  // Folds one load batch (raw 16-byte lane slices of K and V); key u is
+  // valid when bit u of valid_mask is set.
+  __device__ __forceinline__ void consume(const uint4* kr, const uint4* vr, unsigned valid_mask) {
+    constexpr int U = S::kUnroll;
+    float s[U][G];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float kf[EPL];
+      unpack<T>(kr[u], kf);
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float acc = 0.f;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) acc = fmaf(q[g][e], kf[e], acc);
+        acc = group_sum<S::kLPK>(acc);
+        s[u][g] = (valid_mask >> u) & 1u ? acc : kNegInf;
+      }
+    }
+    float mu[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float mt = s[0][g];
+#pragma unroll
+      for (int u = 1; u < U; ++u) mt = fmaxf(mt, s[u][g]);
+      const float mn = fmaxf(m[g], mt);
+      mu[g] = mn == kNegInf ? 0.f : mn;
+      const float alpha = fast_exp2(m[g] - mu[g]);
+      l[g] *= alpha;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) o[g][e] *= alpha;
+      m[g] = mn;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float vf[EPL];
+      unpack<T>(vr[u], vf);
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float pu = fast_exp2(s[u][g] - mu[g]);
+        l[g] += pu;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) o[g][e] = fmaf(pu, vf[e], o[g][e]);
+      }
+    }
+  }
+
+  // Merges the wave's streams (lane groups LPK apart) with butterfly
+  // shuffles; afterwards every group holds the wave's state.
+  __device__ __forceinline__ void merge_wave() {
+#pragma unroll
+    for (int off = S::kLPK; off < 64; off <<= 1) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float m2 = __shfl_xor(m[g], off, 64);
+        const float l2 = __shfl_xor(l[g], off, 64);
+        const float mn = fmaxf(m[g], m2);
+        const float mu = mn == kNegInf ? 0.f : mn;
+        const float w1 = fast_exp2(m[g] - mu);
+        const float w2 = fast_exp2(m2 - mu);
+        l[g] = l[g] * w1 + l2 * w2;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) o[g][e] = o[g][e] * w1 + __shfl_xor(o[g][e], off, 64) * w2;
+        m[g] = mn;
+      }
+    }
+  }
+};
+
+template <typename T, int HD, int G, int W>
+__global__ __launch_bounds__(64 * W) void decode_kernel(const DecodeArgs a) {
+  using S = DecodeShape<T, HD, W>;
+  constexpr int EPL = S::kEPL, LPK = S::kLPK, NS = S::kStreams, U = S::kUnroll, STEP = S::kStep;
   const asrattn_decode_params& p = a.p;
 
   const int split = blockIdx.x;
@@ -90,120 +173,87 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split_kernel(const Deco
   const int k0 = min(n, split * chunk);
   const int k1 = min(n, k0 + chunk);
 
-  // Queries of the G heads sharing kv head hkv, pre-scaled into base 2.
-  float q[G][EPL];
+  Stream<T, HD, G, W> st;
   {
     const T* qp = static_cast<const T*>(p.q) + (int64_t)b * p.q_batch_stride +
                   (int64_t)hkv * G * p.q_head_stride + sub * EPL;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      unpack<T>(load_vec(qp + (int64_t)g * p.q_head_stride), q[g]);
+      unpack<T>(*reinterpret_cast<const uint4*>(qp + (int64_t)g * p.q_head_stride), st.q[g]);
 #pragma unroll
-      for (int e = 0; e < EPL; ++e) q[g][e] *= a.c;
+      for (int e = 0; e < EPL; ++e) st.q[g][e] *= a.c;
     }
   }
-
-  float m[G], l[G], o[G][EPL];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    m[g] = kNegInf;
-    l[g] = 0.f;
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) o[g][e] = 0.f;
-  }
+  st.init();
 
   const T* kp = static_cast<const T*>(p.k) + (int64_t)b * p.k_batch_stride +
                 (int64_t)hkv * p.k_head_stride + sub * EPL;
   const T* vp = static_cast<const T*>(p.v) + (int64_t)b * p.v_batch_stride +
                 (int64_t)hkv * p.v_head_stride + sub * EPL;
 
-  for (int base = k0; base < k1; base += NS * U) {
-    uint4 kr[U], vr[U];
+  // Key u of the batch starting at `base` is base + u * NS + stream.
+  auto load = [&](uint4* kr, uint4* vr, int base) -> unsigned {
+    unsigned mask = 0;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int j = base + u * NS + stream;
       if (j < k1) {
-        kr[u] = load_vec(kp + (int64_t)j * p.k_token_stride);
-        vr[u] = load_vec(vp + (int64_t)j * p.v_token_stride);
+        kr[u] = *reinterpret_cast<const uint4*>(kp + (int64_t)j * p.k_token_stride);
+        vr[u] = *reinterpret_cast<const uint4*>(vp + (int64_t)j * p.v_token_stride);
+        mask |= 1u << u;
       } else {
         kr[u] = make_uint4(0, 0, 0, 0);
         vr[u] = make_uint4(0, 0, 0, 0);
       }
     }
+    return mask;
+  };
 
-    float s[U][G];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      float kf[EPL];
-      unpack<T>(kr[u], kf);
-      const bool valid = base + u * NS + stream < k1;
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        float acc = 0.f;
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) acc = fmaf(q[g][e], kf[e], acc);
-        acc = group_sum<LPK>(acc);
-        s[u][g] = valid ? acc : kNegInf;
-      }
-    }
-
-    float mu[G];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float mt = s[0][g];
-#pragma unroll
-      for (int u = 1; u < U; ++u) mt = fmaxf(mt, s[u][g]);
-      const float mn = fmaxf(m[g], mt);
-      mu[g] = mn == kNegInf ? 0.f : mn;
-      const float alpha = fast_exp2(m[g] - mu[g]);
-      l[g] *= alpha;
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) o[g][e] *= alpha;
-      m[g] = mn;
-    }
-
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      float vf[EPL];
-      unpack<T>(vr[u], vf);
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const float pu = fast_exp2(s[u][g] - mu[g]);
-        l[g] += pu;
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) o[g][e] = fmaf(pu, vf[e], o[g][e]);
-      }
-    }
+  // Two register batches in ping-pong: the next batch is in flight while the
+  // current one is consumed.
+  uint4 ka[U], va[U], kb[U], vb[U];
+  unsigned ma = 0, mb = 0;
+  if (k0 < k1) ma = load(ka, va, k0);
+  for (int base = k0; base < k1; base += 2 * STEP) {
+    if (base + STEP < k1) mb = load(kb, vb, base + STEP);
+    st.consume(ka, va, ma);
+    if (base + STEP >= k1) break;
+    if (base + 2 * STEP < k1) ma = load(ka, va, base + 2 * STEP);
+    st.consume(kb, vb, mb);
   }
 
-  // Merge the workgroup's streams.
-  __shared__ float sm_m[NS][G];
-  __shared__ float sm_l[NS][G];
-  __shared__ float sm_o[NS][G][HD];
-  if (sub == 0) {
+  st.merge_wave();
+
+  // Merge the waves in LDS.
+  __shared__ float sm_m[W][G];
+  __shared__ float sm_l[W][G];
+  __shared__ float sm_o[W][G][HD];
+  if (lane < LPK) {
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      sm_m[stream][g] = m[g];
-      sm_l[stream][g] = l[g];
+      if (lane == 0) {
+        sm_m[wave][g] = st.m[g];
+        sm_l[wave][g] = st.l[g];
+      }
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) sm_o[wave][g][sub * EPL + e] = st.o[g][e];
     }
   }
-#pragma unroll
-  for (int g = 0; g < G; ++g)
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) sm_o[stream][g][sub * EPL + e] = o[g][e];
   __syncthreads();
 
   for (int t = threadIdx.x; t < G * HD; t += S::kThreads) {
     const int g = t / HD;
     const int d = t % HD;
     float mx = kNegInf;
-    for (int s2 = 0; s2 < NS; ++s2) mx = fmaxf(mx, sm_m[s2][g]);
+#pragma unroll
+    for (int w = 0; w < W; ++w) mx = fmaxf(mx, sm_m[w][g]);
     const float mxu = mx == kNegInf ? 0.f : mx;
     float lsum = 0.f, osum = 0.f;
-    for (int s2 = 0; s2 < NS; ++s2) {
-      const float w = fast_exp2(sm_m[s2][g] - mxu);
-      lsum = fmaf(sm_l[s2][g], w, lsum);
-      osum = fmaf(sm_o[s2][g][d], w, osum);
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      const float wt = fast_exp2(sm_m[w][g] - mxu);
+      lsum = fmaf(sm_l[w][g], wt, lsum);
+      osum = fmaf(sm_o[w][g][d], wt, osum);
     }
     const int hq = hkv * G + g;
     if (a.splits == 1) {
@@ -241,24 +291,32 @@ __global__ __launch_bounds__(HD) void decode_combine_kernel(const DecodeArgs a) 
   Elem<T>::store1(op, lsum > 0.f ? osum / lsum : 0.f);
 }
 
-template <typename T, int HD, int G>
+template <typename T, int HD, int G, int W>
 hipError_t launch_typed(const DecodeArgs& a, hipStream_t stream) {
-  using S = DecodeShape<T, HD>;
   const asrattn_decode_params& p = a.p;
   dim3 grid(a.splits, p.heads_kv, p.batch);
-  hipLaunchKernelGGL((decode_split_kernel<T, HD, G>), grid, dim3(S::kThreads), 0, stream, a);
+  hipLaunchKernelGGL((decode_kernel<T, HD, G, W>), grid, dim3(64 * W), 0, stream, a);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || a.splits == 1) return err;
   hipLaunchKernelGGL((decode_combine_kernel<T, HD>), dim3(p.heads_q, p.batch), dim3(HD), 0, stream, a);
   return hipGetLastError();
 }
 
+template <typename T, int HD, int G>
+hipError_t launch_waves(const DecodeArgs& a, int waves, hipStream_t stream) {
+  switch (waves) {
+    case 4: return launch_typed<T, HD, G, 4>(a, stream);
+    case 8: return launch_typed<T, HD, G, 8>(a, stream);
+    default: return launch_typed<T, HD, G, 16>(a, stream);
+  }
+}
+
 template <typename T, int HD>
-hipError_t launch_hd(const DecodeArgs& a, int group, hipStream_t stream) {
+hipError_t launch_hd(const DecodeArgs& a, int group, int waves, hipStream_t stream) {
   switch (group) {
-    case 1: return launch_typed<T, HD, 1>(a, stream);
-    case 2: return launch_typed<T, HD, 2>(a, stream);
-    case 4: return launch_typed<T, HD, 4>(a, stream);
+    case 1: return launch_waves<T, HD, 1>(a, waves, stream);
+    case 2: return launch_waves<T, HD, 2>(a, waves, stream);
+    case 4: return launch_waves<T, HD, 4>(a, waves, stream);
     default: return hipErrorInvalidValue;
   }
 }
@@ -272,6 +330,18 @@ bool decode_supported(int dtype, int head_dim, int group) {
   return dt && hd && g;
 }
 
+int decode_waves(const asrattn_decode_params& p, int splits) {
+  // Enough waves in flight to keep HBM busy: about 16 per CU over the grid,
+  // but no more waves than key rows a load batch can use.
+  const long long groups = (long long)p.batch * p.heads_kv * splits;
+  const int keys_per_split = (p.max_len_k + splits - 1) / splits;
+  int waves = groups >= 1024 ? 4 : groups >= 384 ? 8 : 16;
+  // A wave loads 64 / LPK rows per instruction (8 for bf16 x 64, 4 for 128).
+  const int rows_per_wave = 64 / (p.head_dim * (p.dtype == ASRATTN_BF16 ? 2 : 4) / 16);
+  while (waves > 4 && waves * rows_per_wave * 2 > keys_per_split) waves /= 2;
+  return waves;
+}
+
 hipError_t launch_decode(const asrattn_decode_params& p, int splits, float* ws_o, float* ws_ml,
                          hipStream_t stream) {
   DecodeArgs a;
@@ -281,12 +351,13 @@ hipError_t launch_decode(const asrattn_decode_params& p, int splits, float* ws_o
   a.splits = splits;
   a.c = p.scale * kLog2e;
   const int group = p.heads_q / p.heads_kv;
+  const int waves = decode_waves(p, splits);
   if (p.dtype == ASRATTN_BF16) {
-    return p.head_dim == 64 ? launch_hd<bf16_raw, 64>(a, group, stream)
-                            : launch_hd<bf16_raw, 128>(a, group, stream);
+    return p.head_dim == 64 ? launch_hd<bf16_raw, 64>(a, group, waves, stream)
+                            : launch_hd<bf16_raw, 128>(a, group, waves, stream);
   }
-  return p.head_dim == 64 ? launch_hd<float, 64>(a, group, stream)
-                          : launch_hd<float, 128>(a, group, stream);
+  return p.head_dim == 64 ? launch_hd<float, 64>(a, group, waves, stream)
+                          : launch_hd<float, 128>(a, group, waves, stream);
 }
 
 }  // namespace asrattn

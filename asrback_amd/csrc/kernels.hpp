@@ -8,11 +8,13 @@
 
 namespace asrattn {
 
-// Decoder step: split-K pass (and, for num_splits > 1, the combine pass).
-// ws_o / ws_ml are the workspace: float[batch][heads_q][splits][head_dim] and
-// float[batch][heads_q][splits][2].
+// Decoder step over `splits` workgroups per (sequence, kv head); for
+// splits > 1 the workspace holds the partial outputs
+// float[batch][heads_q][splits][head_dim] and (max, sum) pairs
+// float[batch][heads_q][splits][2], merged by a second kernel.
 hipError_t launch_decode(const asrattn_decode_params& p, int splits, float* ws_o, float* ws_ml,
                          hipStream_t stream);
+int decode_waves(const asrattn_decode_params& p, int splits);
 bool decode_supported(int dtype, int head_dim, int group);
 
 // Multi-row forward on matrix cores (bf16, head_dim 64 or 128).

@@ -250,6 +250,29 @@ class WhisperSmallDecoderStep(Workload):
                 "layers": self.layers, "self_keys": "U{1..224} in a 256 bucket", "cross_frames": 1500}
 
 
+class CopyCalibration(Workload):
+    """A plain device-to-device copy of 1 GiB: the known-size kernel that
+    scales the HBM traffic counters (FETCH_SIZE / WRITE_SIZE)."""
+
+    name = "copy-1GiB"
+    unit = "GB/s"
+    bound = "hbm"
+    kernel = "copy"
+
+    def __init__(self, torch, attention) -> None:
+        del attention
+        self.src = torch.ones(1 << 29, dtype=torch.bfloat16, device="cuda")
+        self.dst = torch.empty_like(self.src)
+        self.launches = 1
+        self.work_per_step = 2.0 * (1 << 30)  # read + write
+
+    def run(self) -> None:
+        self.dst.copy_(self.src)
+
+    def config(self) -> dict:
+        return {"workload": self.name, "bytes_read": 1 << 30, "bytes_written": 1 << 30}
+
+
 def time_graph(torch, workload: Workload, steps: int, warmup: int, reset=None) -> float:
     """Milliseconds per step: the step captured once as a hipGraph, ``warmup``
     untimed replays, then ``steps`` replays between HIP events on the
@@ -374,7 +397,7 @@ def main() -> int:
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--no-cpu-baseline", action="store_true")
-    parser.add_argument("--only", choices=["sensevoice", "turbo", "qwen3", "whisper-small"], default=None,
+    parser.add_argument("--only", choices=["sensevoice", "turbo", "qwen3", "whisper-small", "copy"], default=None,
                         help="measure one workload only (for profiling)")
     args = parser.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -399,6 +422,7 @@ def main() -> int:
         "turbo": WhisperTurboEncoder,
         "qwen3": Qwen3Decode,
         "whisper-small": WhisperSmallDecoderStep,
+        "copy": CopyCalibration,
     }
     if args.only:
         workload = selected[args.only](torch, attention)

@@ -111,8 +111,10 @@ typedef struct asrattn_fwd_params {
 int asrattn_fwd(const asrattn_fwd_params* params, void* stream);
 
 /*
- * One query per sequence over a key/value cache (decoder step), split over
- * the keys (split-K) and combined in a second pass.
+ * One query per sequence over a key/value cache (decoder step).  A
+ * workgroup streams the keys of one (sequence, kv head); when the batch has
+ * too few of those to fill the GPU, the keys are split over several
+ * workgroups (split-K) and a second kernel merges their partials.
  *
  *   out[b, h, :] = softmax_j(scale * q[b, h, :] . k[b, j, h / g, :]) v[b, j, h / g, :]
  *   for j < n_b,  n_b = min(max_len_k, seqused_k[b])      (seqused_k given)
@@ -125,7 +127,8 @@ int asrattn_fwd(const asrattn_fwd_params* params, void* stream);
  * (batch, 1024, kv_heads, head_dim) for Qwen3-ASR.
  *
  * workspace: device memory of asrattn_decode_workspace_size(params) bytes
- * (0 when a single split is used), owned by the caller; it must stay valid
+ * (0 when a single split is used), 256-byte aligned, owned by the caller;
+ * it holds the split partials, needs no initialization, must stay valid
  * until the launch completes and must not be shared by concurrent calls.
  *
  * Replaces:

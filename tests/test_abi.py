@@ -127,12 +127,22 @@ def test_workspace_size_and_split_choice(lib):
     from asrback_amd import _lib
 
     p = _lib.DecodeParams()
-    # Whisper-small cross-attention: 16 rows x 12 heads over 1500 frames.
+    # Whisper-small cross-attention: 16 rows x 12 heads over 1500 frames is
+    # enough (sequence, head) pairs for one split; whisper-tiny's batch of one
+    # (6 heads) splits its keys.
     p.batch, p.heads_q, p.heads_kv, p.head_dim, p.max_len_k = 16, 12, 12, 64, 1500
     p.dtype, p.scale = _lib.BF16, 0.125
+    assert lib.asrattn_decode_num_splits(ctypes.byref(p)) == 1
+    assert lib.asrattn_decode_workspace_size(ctypes.byref(p)) == 0
+    p.batch, p.heads_q, p.heads_kv = 1, 6, 6
     splits = lib.asrattn_decode_num_splits(ctypes.byref(p))
-    assert splits > 1
-    assert lib.asrattn_decode_workspace_size(ctypes.byref(p)) == 16 * 12 * splits * (64 + 2) * 4
+    assert splits == 6  # 1500 keys, at least 256 per split
+
+    def up(n):
+        return (n + 255) // 256 * 256
+
+    rows = 6 * splits
+    assert lib.asrattn_decode_workspace_size(ctypes.byref(p)) == up(rows * 64 * 4) + up(rows * 8)
     p.num_splits = 1
     assert lib.asrattn_decode_workspace_size(ctypes.byref(p)) == 0
     assert lib.asrattn_decode_num_splits(ctypes.byref(p)) == 1

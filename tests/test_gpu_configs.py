@@ -1,0 +1,245 @@
+"""GPU parity at the reference's configuration shapes, edge cases and graph
+replays, against the CPU oracle (torch SDPA with the reference's masks) on
+the same inputs.
+
+Bar: max |out - ref| / max |ref| <= 1e-5 (fp32) and <= 2e-2 (bf16, against
+an fp32 reference on the bf16-rounded inputs).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import max_rel_err
+from oracle import attention as oa
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float32: 1e-5, torch.bfloat16: 2e-2}
+
+
+@pytest.fixture(scope="module")
+def ops():
+    from asrback_amd import attention
+
+    return attention
+
+
+def say(*args):
+    print(*args, flush=True)
+
+
+def randn(*shape, seed, dtype=torch.float32):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(*shape, generator=g).to(dtype)
+
+
+# --- encoder self-attention ----------------------------------------------------
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_sensevoice_ragged_batch(ops, device, dtype):
+    """SenseVoice SAN-M: B=32, 4 x 128, lengths 4 + U{100..500}, key padding
+    through seqused_k on views of the fused (B, L, 1536) projection
+    (sensevoice.py:97, :110-133)."""
+    say("sensevoice ragged", dtype)
+    rng = np.random.default_rng(11)
+    lengths = torch.from_numpy((rng.integers(100, 501, size=32) + 4).astype(np.int32))
+    length = int(lengths.max())
+    fused = randn(32, length, 1536, seed=11, dtype=dtype)
+    ref = oa.sensevoice_attention(fused.float(), 4, oa.key_padding_mask(lengths, length))
+    x = fused.to(device)
+    q, k, v = (t.view(32, length, 4, 128) for t in x.split(512, dim=-1))
+    out = ops.flash(q, k, v, seqused_k=lengths.to(device))
+    assert max_rel_err(out.reshape(32, length, 512), ref) < TOL[dtype]
+
+
+def test_sensevoice_unmasked_equals_masked_full_length(ops, device):
+    """No mask when every row is full length (sensevoice.py:99-103, :550)."""
+    x = randn(3, 130, 1536, seed=12, dtype=torch.bfloat16).to(device)
+    q, k, v = (t.view(3, 130, 4, 128) for t in x.split(512, dim=-1))
+    full = ops.flash(q, k, v)
+    masked = ops.flash(q, k, v, seqused_k=torch.full((3,), 130, dtype=torch.int32, device=device))
+    assert torch.equal(full, masked)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_whisper_encoder_shapes(ops, device, dtype):
+    """Whisper encoder self-attention over 1500 frames: large-v3-turbo's 20
+    heads x 64 (2 of its 16 rows) in bf16, and whisper-tiny's 6 heads in fp32
+    (whisper.py:102-110)."""
+    heads = 20 if dtype == torch.bfloat16 else 6
+    batch = 2 if dtype == torch.bfloat16 else 1
+    say("whisper encoder", dtype, heads)
+    x = randn(batch, 1500, 3 * heads * 64, seed=13, dtype=dtype)
+    q, k, v = (oa.split_heads(t, heads) for t in x.float().split(heads * 64, dim=-1))
+    ref = oa.sdpa(q, k, v)
+    xd = x.to(device)
+    qd, kd, vd = (oa.split_heads(t, heads) for t in xd.split(heads * 64, dim=-1))
+    out = ops.sdpa(qd, kd, vd)  # (B, L, H, D)
+    assert max_rel_err(out.transpose(1, 2), ref) < TOL[dtype]
+
+
+@pytest.mark.parametrize("length", [1, 2, 31, 63, 64, 65, 127, 129, 448])
+def test_causal_prefix_lengths(ops, device, length):
+    """Causal prompt prefix, q len == k len (whisper.py:229-237)."""
+    say("causal prefix", length)
+    q, k, v = (randn(3, 6, length, 64, seed=14 + i, dtype=torch.bfloat16) for i in range(3))
+    ref = oa.sdpa(q.float(), k.float(), v.float(), is_causal=length > 1)
+    out = ops.sdpa(q.to(device), k.to(device), v.to(device), is_causal=length > 1)
+    assert max_rel_err(out.transpose(1, 2), ref) < 2e-2
+
+
+def test_qwen_packed_causal_prefill(ops, device):
+    """Qwen3 prompts packed back to back, causal GQA 16/8 x 128
+    (qwen3_asr.py:152-181, :374-390)."""
+    lengths = [417, 402, 430, 425]
+    tokens = sum(lengths)
+    q = randn(tokens, 16, 128, seed=15, dtype=torch.bfloat16)
+    k = randn(tokens, 8, 128, seed=16, dtype=torch.bfloat16)
+    v = randn(tokens, 8, 128, seed=17, dtype=torch.bfloat16)
+    segments = oa.Segments.from_lengths(lengths)
+    ref = oa.qwen_attend(q.float(), k.float(), v.float(), segments, causal=True)
+    starts = segments.starts.to(device)
+    out = ops.varlen_attn(q.to(device), k.to(device), v.to(device), starts, starts, max(lengths),
+                          max(lengths), window_size=(-1, 0), enable_gqa=True)
+    assert max_rel_err(out, ref) < 2e-2
+
+
+def test_qwen_audio_windows_noncausal(ops, device):
+    """Audio encoder windows of <= 104 tokens, non-causal varlen
+    (qwen3_asr.py:216-221, :303-310)."""
+    lengths = [104, 104, 37, 104, 81]
+    tokens = sum(lengths)
+    q, k, v = (randn(tokens, 16, 64, seed=18 + i, dtype=torch.bfloat16) for i in range(3))
+    segments = oa.Segments.from_lengths(lengths)
+    ref = oa.qwen_attend(q.float(), k.float(), v.float(), segments, causal=False)
+    starts = segments.starts.to(device)
+    out = ops.varlen_attn(q.to(device), k.to(device), v.to(device), starts, starts, 104, 104)
+    assert max_rel_err(out, ref) < 2e-2
+
+
+# --- decoder steps ---------------------------------------------------------------
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_whisper_small_decoder_step(ops, device, dtype):
+    """Whisper-small step: 16 rows x 12 heads x 64; self-attention over the
+    256 bucket with keys 0..position (positions U{0..223}), cross-attention
+    over 1500 frames (whisper.py:235-240, mask :263-264)."""
+    say("whisper small step", dtype)
+    rng = np.random.default_rng(19)
+    positions = torch.from_numpy(rng.integers(0, 224, size=16).astype(np.int64))
+    q = randn(16, 12, 1, 64, seed=19, dtype=dtype)
+    cache_k = randn(16, 12, 448, 64, seed=20, dtype=dtype)
+    cache_v = randn(16, 12, 448, 64, seed=21, dtype=dtype)
+    cross_k = randn(16, 12, 1500, 64, seed=22, dtype=dtype)
+    cross_v = randn(16, 12, 1500, 64, seed=23, dtype=dtype)
+    mask = oa.whisper_step_mask(positions, 256)
+    ref_self = oa.sdpa(q.float(), cache_k[:, :, :256].float(), cache_v[:, :, :256].float(), attn_mask=mask)
+    ref_cross = oa.sdpa(q.float(), cross_k.float(), cross_v.float())
+    qd, kd, vd = q.to(device), cache_k.to(device), cache_v.to(device)
+    out_self = ops.sdpa(qd, kd[:, :, :256], vd[:, :, :256], ops.KeyPrefix(positions=positions.to(device)))
+    out_cross = ops.sdpa(qd, cross_k.to(device), cross_v.to(device))
+    assert max_rel_err(out_self.transpose(1, 2), ref_self) < TOL[dtype]
+    assert max_rel_err(out_cross.transpose(1, 2), ref_cross) < TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_qwen_gqa_decode(ops, device, dtype):
+    """Qwen3-1.7B step: 64 rows, 16 query / 8 kv heads x 128 over the
+    (64, 1024, 8, 128) cache with seqused_k = position + 1, positions
+    400-557 (qwen3_asr.py:392-432)."""
+    say("qwen decode", dtype)
+    rng = np.random.default_rng(24)
+    positions = torch.from_numpy((390 + rng.integers(10, 41, size=64) + rng.integers(0, 128, size=64)).astype(np.int64))
+    q = randn(64, 16, 128, seed=24, dtype=dtype)
+    keys = randn(64, 1024, 8, 128, seed=25, dtype=dtype)
+    values = randn(64, 1024, 8, 128, seed=26, dtype=dtype)
+    ref = oa.qwen_step_attention(q.float(), keys.float(), values.float(), oa.qwen_step_mask(positions, 1024))
+    used = (positions + 1).to(torch.int32).to(device)
+    out = ops.decode(q.to(device), keys.to(device), values.to(device), seqused_k=used)
+    assert max_rel_err(out, ref) < TOL[dtype]
+
+
+@pytest.mark.parametrize("splits", [1, 2, 3, 7, 16, 64])
+def test_decode_split_count_does_not_change_result(ops, device, splits):
+    """Any split count gives the same output (the last split merges)."""
+    q = randn(5, 8, 128, seed=27, dtype=torch.bfloat16).to(device)
+    k = randn(5, 700, 4, 128, seed=28, dtype=torch.bfloat16).to(device)
+    v = randn(5, 700, 4, 128, seed=29, dtype=torch.bfloat16).to(device)
+    used = torch.tensor([1, 64, 65, 333, 700], dtype=torch.int32, device=device)
+    base = ops.decode(q, k, v, seqused_k=used, num_splits=1).float()
+    out = ops.decode(q, k, v, seqused_k=used, num_splits=splits).float()
+    assert max_rel_err(out, base) < 1e-2
+
+
+def test_decode_zero_keys_gives_zeros(ops, device):
+    q = randn(3, 4, 64, seed=32).to(device)
+    k = randn(3, 50, 4, 64, seed=33).to(device)
+    used = torch.tensor([0, 5, 0], dtype=torch.int32, device=device)
+    out = ops.decode(q, k, k, seqused_k=used, num_splits=4)
+    assert torch.count_nonzero(out[0]) == 0 and torch.count_nonzero(out[2]) == 0
+    assert torch.count_nonzero(out[1]) > 0
+
+
+def test_encoder_zero_keys_gives_zeros(ops, device):
+    q = randn(2, 40, 2, 128, seed=34, dtype=torch.bfloat16).to(device)
+    used = torch.tensor([0, 17], dtype=torch.int32, device=device)
+    out = ops.flash(q, q, q, seqused_k=used)
+    assert torch.count_nonzero(out[0]) == 0 and torch.count_nonzero(out[1]) > 0
+
+
+def test_step_matches_last_row_of_prefill_on_gpu(ops, device):
+    """Invariant: a decoder step at position p equals row p of the causal
+    prefill over the same keys."""
+    q, k, v = (randn(2, 6, 40, 64, seed=35 + i, dtype=torch.bfloat16).to(device) for i in range(3))
+    full = ops.sdpa(q, k, v, is_causal=True)  # (B, L, H, D)
+    for p in (0, 17, 39):
+        pos = torch.full((2,), p, dtype=torch.int64, device=device)
+        step = ops.sdpa(q[:, :, p : p + 1], k, v, ops.KeyPrefix(positions=pos))
+        assert max_rel_err(step[:, 0].float(), full[:, p].float()) < 2e-2
+
+
+def test_decode_replays_from_a_graph(ops, device):
+    """A captured decode sees new positions on every replay; each replay
+    matches the eager call (graph replays interleaved with eager work)."""
+    q = randn(8, 12, 1, 64, seed=38, dtype=torch.bfloat16).to(device)
+    k = randn(8, 12, 448, 64, seed=39, dtype=torch.bfloat16).to(device)
+    v = randn(8, 12, 448, 64, seed=40, dtype=torch.bfloat16).to(device)
+    positions = torch.zeros(8, dtype=torch.int64, device=device)
+    out = torch.empty(8, 1, 12, 64, dtype=torch.bfloat16, device=device)
+
+    def step():
+        out.copy_(ops.sdpa(q, k[:, :, :256], v[:, :, :256], ops.KeyPrefix(positions=positions)))
+
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for _ in range(3):
+            step()
+    torch.cuda.current_stream().wait_stream(stream)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    rng = np.random.default_rng(41)
+    for _ in range(4):
+        positions.copy_(torch.from_numpy(rng.integers(0, 256, size=8)).to(device))
+        graph.replay()
+        torch.cuda.synchronize()
+        replayed = out.clone()
+        eager = ops.sdpa(q, k[:, :, :256], v[:, :, :256], ops.KeyPrefix(positions=positions))
+        torch.cuda.synchronize()
+        assert torch.equal(replayed, eager)
+
+
+def test_errors_raise_runtime_error(ops, device):
+    from asrback_amd._lib import AttentionError
+
+    q = randn(2, 3, 96, seed=42).to(device)  # head_dim 96: no kernel
+    with pytest.raises(AttentionError, match="head_dim"):
+        ops.decode(q, q[:, None].expand(2, 5, 3, 96), q[:, None].expand(2, 5, 3, 96))
+    with pytest.raises(RuntimeError, match="GPU only"):
+        ops.decode(q.cpu(), q.cpu()[:, None], q.cpu()[:, None])
