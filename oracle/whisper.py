@@ -1,0 +1,286 @@
+"""Whisper restated on the CPU: the network of the reference's
+``models/whisper.py:73-342`` with its SDPA calls and masks, and the greedy
+prompt + step loop of ``whisper.py:828-974`` (temperature 0, one window).
+
+Parameter names match the reference (Hugging Face names), so the same seeded
+state dict loads into this model and into ``asrback_amd.whisper``.
+"""
+
+from __future__ import annotations
+
+import math
+import zlib
+
+import torch
+import torch.nn.functional as F
+from torch import Tensor, nn
+
+from . import attention as oa
+
+# Whisper-tiny's shape (the defaults of Hugging Face's WhisperConfig).
+WHISPER_TINY = {
+    "d_model": 384,
+    "encoder_attention_heads": 6,
+    "decoder_attention_heads": 6,
+    "encoder_layers": 4,
+    "decoder_layers": 4,
+    "encoder_ffn_dim": 1536,
+    "decoder_ffn_dim": 1536,
+    "num_mel_bins": 80,
+    "max_source_positions": 1500,
+    "max_target_positions": 448,
+    "vocab_size": 51865,
+    "eos_token_id": 50257,
+}
+# Multilingual tokenizer ids: <|startoftranscript|>, <|en|>, <|transcribe|>,
+# <|notimestamps|>.
+SOT, EN, TRANSCRIBE, NO_TIMESTAMPS = 50258, 50259, 50359, 50363
+BEGIN_SUPPRESS = (220, 50257)
+
+
+class MultiHeadAttention(nn.Module):
+    """``whisper.py:73-110``."""
+
+    def __init__(self, width: int, heads: int) -> None:
+        super().__init__()
+        self.heads = heads
+        self.k_proj = nn.Linear(width, width, bias=False)
+        self.v_proj = nn.Linear(width, width)
+        self.q_proj = nn.Linear(width, width)
+        self.out_proj = nn.Linear(width, width)
+
+    def project_key_value(self, x: Tensor) -> tuple[Tensor, Tensor]:
+        return oa.split_heads(self.k_proj(x), self.heads), oa.split_heads(self.v_proj(x), self.heads)
+
+    def attend(self, x: Tensor, key: Tensor, value: Tensor, mask=None, is_causal=False) -> Tensor:
+        query = oa.split_heads(self.q_proj(x), self.heads)
+        out = oa.sdpa(query, key, value, attn_mask=mask, is_causal=is_causal)
+        return self.out_proj(out.transpose(1, 2).reshape(x.shape[0], x.shape[1], -1))
+
+    def forward(self, x: Tensor) -> Tensor:
+        return self.attend(x, *self.project_key_value(x))
+
+
+class EncoderLayer(nn.Module):
+    def __init__(self, config: dict) -> None:
+        super().__init__()
+        width = config["d_model"]
+        self.self_attn = MultiHeadAttention(width, config["encoder_attention_heads"])
+        self.self_attn_layer_norm = nn.LayerNorm(width)
+        self.fc1 = nn.Linear(width, config["encoder_ffn_dim"])
+        self.fc2 = nn.Linear(config["encoder_ffn_dim"], width)
+        self.final_layer_norm = nn.LayerNorm(width)
+
+    def forward(self, x: Tensor) -> Tensor:
+        x = x + self.self_attn(self.self_attn_layer_norm(x))
+        return x + self.fc2(F.gelu(self.fc1(self.final_layer_norm(x))))
+
+
+class WhisperEncoder(nn.Module):
+    """``whisper.py:128-153``."""
+
+    def __init__(self, config: dict) -> None:
+        super().__init__()
+        width = config["d_model"]
+        self.conv1 = nn.Conv1d(config["num_mel_bins"], width, 3, padding=1)
+        self.conv2 = nn.Conv1d(width, width, 3, stride=2, padding=1)
+        self.embed_positions = nn.Embedding(config["max_source_positions"], width)
+        self.layers = nn.ModuleList(EncoderLayer(config) for _ in range(config["encoder_layers"]))
+        self.layer_norm = nn.LayerNorm(width)
+
+    def forward(self, mel: Tensor) -> Tensor:
+        x = F.gelu(self.conv1(mel))
+        x = F.gelu(self.conv2(x)).transpose(1, 2).contiguous()
+        x = x + self.embed_positions.weight
+        for layer in self.layers:
+            x = layer(x)
+        return self.layer_norm(x)
+
+
+class DecoderLayer(nn.Module):
+    """``whisper.py:199-241``; ``cache`` is (self_keys, self_values,
+    cross_keys, cross_values) of this layer, ``(B, H, L, D)`` each."""
+
+    def __init__(self, config: dict) -> None:
+        super().__init__()
+        width = config["d_model"]
+        heads = config["decoder_attention_heads"]
+        self.self_attn = MultiHeadAttention(width, heads)
+        self.self_attn_layer_norm = nn.LayerNorm(width)
+        self.encoder_attn = MultiHeadAttention(width, heads)
+        self.encoder_attn_layer_norm = nn.LayerNorm(width)
+        self.fc1 = nn.Linear(width, config["decoder_ffn_dim"])
+        self.fc2 = nn.Linear(config["decoder_ffn_dim"], width)
+        self.final_layer_norm = nn.LayerNorm(width)
+
+    def forward(self, x, cache, positions, length, mask):
+        self_keys, self_values, cross_keys, cross_values = cache
+        hidden = self.self_attn_layer_norm(x)
+        key, value = self.self_attn.project_key_value(hidden)
+        if length is None:
+            index = positions[:, None, None, None].expand_as(key)
+            self_keys.scatter_(2, index, key)
+            self_values.scatter_(2, index, value)
+        else:
+            self_keys.index_copy_(2, positions, key)
+            self_values.index_copy_(2, positions, value)
+            self_keys = self_keys[:, :, :length]
+            self_values = self_values[:, :, :length]
+        x = x + self.self_attn.attend(hidden, self_keys, self_values, mask=mask, is_causal=x.shape[1] > 1)
+        hidden = self.encoder_attn_layer_norm(x)
+        x = x + self.encoder_attn.attend(hidden, cross_keys, cross_values)
+        return x + self.fc2(F.gelu(self.fc1(self.final_layer_norm(x))))
+
+
+class WhisperDecoder(nn.Module):
+    """``whisper.py:244-277``: the step mask is ``key <= position``."""
+
+    def __init__(self, config: dict) -> None:
+        super().__init__()
+        width = config["d_model"]
+        self.embed_tokens = nn.Embedding(config["vocab_size"], width)
+        self.embed_positions = nn.Embedding(config["max_target_positions"], width)
+        self.layers = nn.ModuleList(DecoderLayer(config) for _ in range(config["decoder_layers"]))
+        self.layer_norm = nn.LayerNorm(width)
+
+    def forward(self, tokens, positions, cache, length):
+        mask = None
+        if length is None:
+            x = self.embed_tokens(tokens) + self.embed_positions(positions)[:, None]
+            mask = oa.whisper_step_mask(positions, cache[0].shape[3])
+        else:
+            x = self.embed_tokens(tokens) + self.embed_positions(positions)
+        for index, layer in enumerate(self.layers):
+            x = layer(x, tuple(t[index] for t in cache), positions, length, mask)
+        return self.layer_norm(x)
+
+
+class WhisperModel(nn.Module):
+    def __init__(self, config: dict) -> None:
+        super().__init__()
+        self.encoder = WhisperEncoder(config)
+        self.decoder = WhisperDecoder(config)
+
+
+class WhisperForConditionalGeneration(nn.Module):
+    def __init__(self, config: dict) -> None:
+        super().__init__()
+        self.config = config
+        self.model = WhisperModel(config)
+
+    def allocate_cache(self, batch: int, dtype=torch.float32) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+        """``(layers, B, H, L, D)`` self and cross caches (``whisper.py:293-311``)."""
+        c = self.config
+        heads = c["decoder_attention_heads"]
+        shape = (c["decoder_layers"], batch, heads, 0, c["d_model"] // heads)
+
+        def empty(length):
+            return torch.zeros(shape[:3] + (length,) + shape[4:], dtype=dtype)
+
+        target, source = c["max_target_positions"], c["max_source_positions"]
+        return empty(target), empty(target), empty(source), empty(source)
+
+    def set_encoder_output(self, cache, encoder_output: Tensor) -> None:
+        for index, layer in enumerate(self.model.decoder.layers):
+            key, value = layer.encoder_attn.project_key_value(encoder_output)
+            cache[2][index, : len(encoder_output)] = key
+            cache[3][index, : len(encoder_output)] = value
+
+    def logits(self, hidden: Tensor) -> Tensor:
+        weight = self.model.decoder.embed_tokens.weight
+        rows = hidden.flatten(0, -2)
+        return (weight @ rows.T).T.unflatten(0, hidden.shape[:-1])
+
+
+def suppress_masks(config: dict) -> tuple[Tensor, Tensor]:
+    """Tokens never sampled: every timestamp token (``whisper.py:536-544``);
+    the first step also suppresses the begin tokens."""
+    suppress = torch.zeros(config["vocab_size"], dtype=torch.bool)
+    suppress[NO_TIMESTAMPS + 1 :] = True
+    first = suppress.clone()
+    first[list(BEGIN_SUPPRESS)] = True
+    return suppress, first
+
+
+def choose(logits: Tensor, suppress: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+    """Greedy token and log-probability (``whisper.py:962-974``), plus the gap
+    between the best and second-best logit (how far argmax is from a tie)."""
+    logits = logits.masked_fill(suppress, -math.inf)
+    top2 = logits.topk(2, dim=-1).values
+    token = logits.argmax(dim=-1)
+    logprob = F.log_softmax(logits, dim=-1).gather(1, token[:, None]).squeeze(1)
+    return token, logprob, top2[:, 0] - top2[:, 1]
+
+
+@torch.inference_mode()
+def greedy_decode(model: WhisperForConditionalGeneration, mel: Tensor, steps: int) -> dict:
+    """Encode ``mel`` (B, n_mels, 3000), run the prompt
+    <|startoftranscript|><|en|><|transcribe|><|notimestamps|> and ``steps``
+    tokens in total (the prompt's pick plus ``steps - 1`` decoder steps over
+    the whole self-attention cache), greedy.  Returns the token ids per row
+    and the top-2 logit gap of every pick."""
+    config = model.config
+    batch = mel.shape[0]
+    cache = model.allocate_cache(batch, mel.dtype)
+    model.set_encoder_output(cache, model.model.encoder(mel))
+    suppress, first = suppress_masks(config)
+    prefix = [SOT, EN, TRANSCRIBE, NO_TIMESTAMPS]
+    tokens = torch.tensor([prefix] * batch)
+    length = len(prefix)
+    hidden = model.model.decoder(tokens, torch.arange(length), cache, length)
+    token, _, gap = choose(model.logits(hidden[:, -1]).float(), first)
+    out, gaps = [token], [gap]
+    position = torch.full((batch,), length, dtype=torch.long)
+    for _ in range(steps - 1):
+        hidden = model.model.decoder(token[:, None], position, cache, None)
+        token, _, gap = choose(model.logits(hidden[:, -1]).float(), suppress)
+        out.append(token)
+        gaps.append(gap)
+        position = position + 1
+    return {
+        "tokens": torch.stack(out, dim=1).tolist(),
+        "gaps": torch.stack(gaps, dim=1).tolist(),
+    }
+
+
+def named_weights(module: nn.Module, seed: int) -> dict[str, Tensor]:
+    """A state dict drawn parameter by parameter from generators seeded by
+    (``seed``, parameter name), so it does not depend on registration order:
+    norm weights 1 + N(0, 0.1^2), biases and other vectors N(0, 0.02^2),
+    matrices N(0, 1 / fan_in)."""
+    state = {}
+    for name, param in module.named_parameters():
+        g = torch.Generator().manual_seed((seed * 1_000_003 + zlib.crc32(name.encode())) % (2**62))
+        shape = param.shape
+        if param.dim() == 1 and "norm" in name and name.endswith("weight"):
+            value = 1.0 + 0.1 * torch.randn(shape, generator=g)
+        elif param.dim() == 1:
+            value = 0.02 * torch.randn(shape, generator=g)
+        else:
+            fan_in = math.prod(shape[1:])
+            value = torch.randn(shape, generator=g) / math.sqrt(fan_in)
+        state[name] = value
+    return state
+
+
+def attention_heavy_weights(module: nn.Module, seed: int) -> dict[str, Tensor]:
+    """:func:`named_weights` rescaled so that attention drives the decoder's
+    choices: query/key projections x2, value/output projections x3, MLP x0.5,
+    decoder token and position embeddings x3, LayerNorm biases zero.  With
+    seed 0 and the fixture's log-mel, whisper-tiny's greedy picks vary (8
+    distinct tokens in 32), every pick leads its runner-up by at least 0.09
+    logits, and halving one cross-attention projection changes 25 of the 32
+    picks -- so identical token ids check the attention path."""
+    state = named_weights(module, seed)
+    for name, value in state.items():
+        if "attn." in name and (name.endswith("q_proj.weight") or name.endswith("k_proj.weight")):
+            state[name] = value * 2.0
+        elif "attn." in name and (name.endswith("v_proj.weight") or name.endswith("out_proj.weight")):
+            state[name] = value * 3.0
+        elif name.endswith("fc1.weight") or name.endswith("fc2.weight"):
+            state[name] = value * 0.5
+        elif "decoder.embed_tokens" in name or "decoder.embed_positions" in name:
+            state[name] = value * 3.0
+        elif "norm" in name and name.endswith("bias"):
+            state[name] = torch.zeros_like(value)
+    return state

@@ -14,6 +14,12 @@ reference, at a small size:
     packed     qwen3_asr.py:156-180 (packed causal GQA prefill)
     gqa_step   qwen3_asr.py:414-431 (GQA decode, seqused_k = position + 1)
 
+It also writes ``whisper_tiny_greedy.json``: the greedy token ids the CPU
+oracle (``oracle.whisper``, float32) decodes for whisper-tiny's shape with
+seeded named random weights (``attention_heavy_weights``) and a log-mel input
+drawn from N(0, 1), with the top-2 logit gap of every pick (how far each
+argmax is from a tie).
+
     python tests/golden/make_golden.py
 """
 
@@ -28,6 +34,9 @@ HERE = Path(__file__).resolve().parent
 sys.path.insert(0, str(HERE.parents[1]))
 
 from oracle import brute  # noqa: E402
+
+WHISPER_SEEDS = {"weights": 0, "mel": 1}
+WHISPER_STEPS = 32
 
 
 def bf16_round(x: np.ndarray) -> np.ndarray:
@@ -111,9 +120,40 @@ def cases() -> dict[str, np.ndarray]:
     return out
 
 
+def whisper_mel(seed: int):
+    import torch
+
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(1, 80, 3000, generator=g)
+
+
+def whisper_greedy() -> dict:
+    import torch
+
+    from oracle import whisper as ow
+
+    torch.set_num_threads(min(8, torch.get_num_threads()))
+    model = ow.WhisperForConditionalGeneration(ow.WHISPER_TINY).eval()
+    model.load_state_dict(ow.attention_heavy_weights(model, WHISPER_SEEDS["weights"]))
+    result = ow.greedy_decode(model, whisper_mel(WHISPER_SEEDS["mel"]), WHISPER_STEPS)
+    return {
+        "config": ow.WHISPER_TINY,
+        "seeds": WHISPER_SEEDS,
+        "steps": WHISPER_STEPS,
+        "prefix": [ow.SOT, ow.EN, ow.TRANSCRIBE, ow.NO_TIMESTAMPS],
+        "tokens": result["tokens"][0],
+        "top2_gaps": [round(g, 6) for g in result["gaps"][0]],
+    }
+
+
 def main() -> None:
+    import json
+
     path = HERE / "attention_cases.npz"
     np.savez_compressed(path, **cases())
+    print(path)
+    path = HERE / "whisper_tiny_greedy.json"
+    path.write_text(json.dumps(whisper_greedy(), indent=1) + "\n")
     print(path)
 
 

@@ -1,0 +1,118 @@
+"""GPU: Whisper on the HIP attention kernels (``asrback_amd.whisper``).
+
+The seeded float32 whisper-tiny model must decode exactly the committed
+greedy token ids of the CPU oracle (``tests/golden/whisper_tiny_greedy.json``)
+-- with the decoder step replayed from hipGraphs per (batch, KV) bucket and
+eagerly; both paths must agree token for token.  Encoder and decoder hidden
+states are compared with the oracle within 1e-4 relative (fp32 GEMMs and
+LayerNorms differ from the CPU's in summation order; attention alone is held
+to 1e-5 in test_gpu_configs).
+"""
+
+from __future__ import annotations
+
+import json
+
+import pytest
+import torch
+
+from conftest import GOLDEN, max_rel_err
+from oracle import whisper as ow
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def fixture():
+    return json.loads((GOLDEN / "whisper_tiny_greedy.json").read_text())
+
+
+@pytest.fixture(scope="module")
+def weights(fixture):
+    model = ow.WhisperForConditionalGeneration(fixture["config"])
+    return ow.attention_heavy_weights(model, fixture["seeds"]["weights"])
+
+
+def mel_for(seed: int) -> torch.Tensor:
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(1, 80, 3000, generator=g)
+
+
+def gpu_model(fixture, weights, device, dtype=torch.float32):
+    from asrback_amd import whisper as aw
+
+    model = aw.WhisperForConditionalGeneration(fixture["config"])
+    model.load_state_dict(weights, strict=True)
+    return model.eval().to(device, dtype)
+
+
+def decoder(model, fixture, device, batch, graphs):
+    from asrback_amd import whisper as aw
+
+    suppress, first = ow.suppress_masks(fixture["config"])
+    return aw.GreedyDecoder(model, batch, suppress, first, fixture["config"]["eos_token_id"], graphs=graphs)
+
+
+def run_rows(dec, model, mels, fixture, device):
+    with torch.inference_mode():
+        encoded = model.model.encoder(torch.cat(mels).to(device, next(model.parameters()).dtype))
+        slots = dec.admit(encoded, [fixture["prefix"]] * len(mels), fixture["steps"])
+        done = {}
+        for _ in range(64):
+            dec.advance()
+            done.update(dec.finished_rows())
+            if len(done) == len(slots):
+                break
+    return [done[s] for s in slots]
+
+
+@pytest.mark.parametrize("graphs", [True, False])
+def test_greedy_tokens_match_oracle_fixture(fixture, weights, device, graphs):
+    print("whisper greedy, graphs =", graphs, flush=True)
+    model = gpu_model(fixture, weights, device)
+    dec = decoder(model, fixture, device, batch=1, graphs=graphs)
+    (tokens,) = run_rows(dec, model, [mel_for(fixture["seeds"]["mel"])], fixture, device)
+    assert tokens == fixture["tokens"]
+
+
+def test_batch_rows_decode_independently(fixture, weights, device):
+    """Two windows in one batch: the fixture's window decodes to the fixture
+    tokens whatever shares its batch."""
+    print("whisper batch of two", flush=True)
+    model = gpu_model(fixture, weights, device)
+    dec = decoder(model, fixture, device, batch=4, graphs=True)
+    rows = run_rows(dec, model, [mel_for(fixture["seeds"]["mel"]), mel_for(77)], fixture, device)
+    assert rows[0] == fixture["tokens"]
+    assert rows[1] != fixture["tokens"]
+
+
+def test_encoder_and_prefix_hidden_states_match_oracle(fixture, weights, device):
+    print("whisper hidden states", flush=True)
+    torch.set_num_threads(min(8, torch.get_num_threads()))
+    ref = ow.WhisperForConditionalGeneration(fixture["config"]).eval()
+    ref.load_state_dict(weights)
+    model = gpu_model(fixture, weights, device)
+    mel = mel_for(fixture["seeds"]["mel"])
+    with torch.inference_mode():
+        enc_ref = ref.model.encoder(mel)
+        enc = model.model.encoder(mel.to(device))
+        assert max_rel_err(enc.cpu(), enc_ref) < 1e-4
+        cache_ref = ref.allocate_cache(1)
+        ref.set_encoder_output(cache_ref, enc_ref)
+        prefix = torch.tensor([fixture["prefix"]])
+        hid_ref = ref.model.decoder(prefix, torch.arange(4), cache_ref, 4)
+        cache = model.allocate_cache(1)
+        model.set_encoder_output(cache, enc)
+        hid = model.decode(prefix.to(device), torch.arange(4, device=device), cache, length=4)
+        assert max_rel_err(hid.cpu(), hid_ref) < 1e-4
+
+
+def test_bf16_model_decodes(fixture, weights, device):
+    """bfloat16 (the reference's CUDA default) runs the same path, graphs
+    included; its tokens need not equal the float32 ones."""
+    print("whisper bf16", flush=True)
+    model = gpu_model(fixture, weights, device, torch.bfloat16)
+    dec = decoder(model, fixture, device, batch=1, graphs=True)
+    (tokens,) = run_rows(dec, model, [mel_for(fixture["seeds"]["mel"])], fixture, device)
+    assert len(tokens) == fixture["steps"]
+    assert all(0 <= t < fixture["config"]["vocab_size"] for t in tokens)

@@ -1,0 +1,48 @@
+"""CPU: the Whisper restatement in the oracle reproduces the committed greedy
+token fixture, and its decoder steps are invariant to the cache length
+they run over (the reference's KV buckets, ``whisper.py:54``, ``:893-896``).
+"""
+
+from __future__ import annotations
+
+import json
+
+import pytest
+import torch
+
+from conftest import GOLDEN, max_rel_err
+from oracle import attention as oa
+from oracle import whisper as ow
+
+
+@pytest.fixture(scope="module")
+def fixture():
+    return json.loads((GOLDEN / "whisper_tiny_greedy.json").read_text())
+
+
+def test_fixture_is_not_degenerate(fixture):
+    assert len(fixture["tokens"]) == fixture["steps"] == 32
+    assert len(set(fixture["tokens"])) >= 5
+    assert min(fixture["top2_gaps"]) > 0.05  # far from argmax ties
+
+
+def test_oracle_reproduces_greedy_fixture(fixture):
+    torch.set_num_threads(min(8, torch.get_num_threads()))
+    model = ow.WhisperForConditionalGeneration(fixture["config"]).eval()
+    model.load_state_dict(ow.attention_heavy_weights(model, fixture["seeds"]["weights"]))
+    g = torch.Generator().manual_seed(fixture["seeds"]["mel"])
+    mel = torch.randn(1, 80, 3000, generator=g)
+    result = ow.greedy_decode(model, mel, fixture["steps"])
+    assert result["tokens"][0] == fixture["tokens"]
+
+
+def test_step_attention_is_bucket_invariant():
+    """A decoder step over a 64-slot view equals one over the whole 448-slot
+    cache: masked slots contribute nothing."""
+    g = torch.Generator().manual_seed(9)
+    q = torch.randn(2, 6, 1, 64, generator=g, dtype=torch.float64)
+    k, v = (torch.randn(2, 6, 448, 64, generator=g, dtype=torch.float64) for _ in range(2))
+    positions = torch.tensor([5, 63])
+    short = oa.sdpa(q, k[:, :, :64], v[:, :, :64], attn_mask=oa.whisper_step_mask(positions, 64))
+    full = oa.sdpa(q, k, v, attn_mask=oa.whisper_step_mask(positions, 448))
+    assert max_rel_err(short, full) < 1e-12
