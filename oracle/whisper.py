@@ -9,13 +9,13 @@ state dict loads into this model and into ``asrback_amd.whisper``.
 from __future__ import annotations
 
 import math
-import zlib
 
 import torch
 import torch.nn.functional as F
 from torch import Tensor, nn
 
 from . import attention as oa
+from .weights import named_weights
 
 # Whisper-tiny's shape (the defaults of Hugging Face's WhisperConfig).
 WHISPER_TINY = {
@@ -241,26 +241,6 @@ def greedy_decode(model: WhisperForConditionalGeneration, mel: Tensor, steps: in
         "tokens": torch.stack(out, dim=1).tolist(),
         "gaps": torch.stack(gaps, dim=1).tolist(),
     }
-
-
-def named_weights(module: nn.Module, seed: int) -> dict[str, Tensor]:
-    """A state dict drawn parameter by parameter from generators seeded by
-    (``seed``, parameter name), so it does not depend on registration order:
-    norm weights 1 + N(0, 0.1^2), biases and other vectors N(0, 0.02^2),
-    matrices N(0, 1 / fan_in)."""
-    state = {}
-    for name, param in module.named_parameters():
-        g = torch.Generator().manual_seed((seed * 1_000_003 + zlib.crc32(name.encode())) % (2**62))
-        shape = param.shape
-        if param.dim() == 1 and "norm" in name and name.endswith("weight"):
-            value = 1.0 + 0.1 * torch.randn(shape, generator=g)
-        elif param.dim() == 1:
-            value = 0.02 * torch.randn(shape, generator=g)
-        else:
-            fan_in = math.prod(shape[1:])
-            value = torch.randn(shape, generator=g) / math.sqrt(fan_in)
-        state[name] = value
-    return state
 
 
 def attention_heavy_weights(module: nn.Module, seed: int) -> dict[str, Tensor]:

@@ -1,0 +1,232 @@
+"""GPU: the SenseVoice and Qwen3-ASR modules on the HIP kernels against their
+CPU restatements in the oracle, with the same seeded named weights.
+
+Whole-module outputs include GEMMs, norms and convolutions that run in a
+different summation order on the GPU, so float32 module outputs are held to
+1e-4 relative (the attention kernels alone meet 1e-5 in test_gpu_configs);
+structural invariants (padding, GQA mask forms, graph replay) are held
+tighter where the arithmetic is identical.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from conftest import max_rel_err
+from oracle import attention as oa
+from oracle import qwen3 as oq
+from oracle import sensevoice as osv
+from oracle.weights import named_weights
+
+pytestmark = pytest.mark.gpu
+
+SENSEVOICE = {
+    "output_size": 512,
+    "attention_heads": 4,
+    "linear_units": 2048,
+    "kernel_size": 11,
+    "num_blocks": 2,
+    "tp_blocks": 1,
+}
+QWEN3 = {
+    "hidden_size": 512,
+    "head_dim": 128,
+    "num_attention_heads": 4,
+    "num_key_value_heads": 2,
+    "intermediate_size": 1024,
+    "num_hidden_layers": 2,
+    "vocab_size": 1000,
+    "rms_norm_eps": 1e-6,
+    "rope_theta": 1e6,
+}
+
+
+def say(*args):
+    print(*args, flush=True)
+
+
+# --- SenseVoice ----------------------------------------------------------------
+
+
+def sensevoice_pair(device):
+    from asrback_amd import sensevoice as asv
+
+    ref = osv.SenseVoiceEncoder(560, SENSEVOICE).eval()
+    state = named_weights(ref, 5)
+    ref.load_state_dict(state)
+    model = asv.SenseVoiceEncoder(560, SENSEVOICE)
+    model.load_state_dict(state, strict=True)
+    return ref, model.eval().to(device)
+
+
+def test_sensevoice_encoder_matches_oracle(device):
+    """Padded ragged batch with the frame mask (sensevoice.py:543-561)."""
+    say("sensevoice encoder")
+    ref, model = sensevoice_pair(device)
+    frames = torch.tensor([80, 40, 120, 7])
+    g = torch.Generator().manual_seed(6)
+    x = torch.randn(4, 4 + 120, 560, generator=g)
+    mask = osv.frame_mask(frames, 4, 120)
+    with torch.inference_mode():
+        expected = ref(x, mask)
+        out = model(x.to(device), mask.to(device))
+    valid = mask[..., None]
+    assert max_rel_err(out.cpu() * valid, expected * valid) < 1e-4
+
+
+def test_sensevoice_padding_invariance(device):
+    """A padded batch gives each row what it gets alone (docs/architecture.md:427-429)."""
+    say("sensevoice padding invariance")
+    _, model = sensevoice_pair(device)
+    frames = [60, 23, 91]
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(3, 4 + 91, 560, generator=g)
+    for b, n in enumerate(frames):
+        x[b, 4 + n :] = 0
+    mask = osv.frame_mask(torch.tensor(frames), 4, 91).to(device)
+    with torch.inference_mode():
+        batched = model(x.to(device), mask)
+        for b, n in enumerate(frames):
+            alone = model(x[b : b + 1, : 4 + n].to(device), None)
+            assert max_rel_err(batched[b, : 4 + n].cpu(), alone[0].cpu()) < 1e-5
+
+
+# --- Qwen3-ASR -------------------------------------------------------------------
+
+
+def qwen_pair(device):
+    from asrback_amd import qwen3_asr as aq
+
+    ref = oq.TextModel(QWEN3).eval()
+    state = named_weights(ref, 8)
+    ref.load_state_dict(state)
+    model = aq.TextModel(QWEN3)
+    model.load_state_dict(state, strict=True)
+    return ref, model.eval().to(device)
+
+
+def test_qwen_prefill_and_steps_match_oracle(device):
+    """Packed causal GQA prefill into cache rows, then decoder steps over the
+    cache with seqused_k = position + 1 (qwen3_asr.py:374-432, :472-524)."""
+    from asrback_amd import qwen3_asr as aq
+
+    say("qwen3 prefill + steps")
+    ref, model = qwen_pair(device)
+    lengths = [37, 52, 29]
+    rows = [2, 0, 1]
+    batch, cache_len = 3, 128
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(sum(lengths), QWEN3["hidden_size"], generator=g)
+    row_ids = torch.cat([torch.full((n,), r) for n, r in zip(lengths, rows)])
+    positions = torch.cat([torch.arange(n) for n in lengths])
+    cos, sin = oa.rope_tables(QWEN3["rope_theta"], 128, cache_len, torch.float32)
+    shape = (2, batch, cache_len, 2, 128)
+    keys_ref, values_ref = torch.zeros(shape), torch.zeros(shape)
+    cache = aq.KVCache.allocate(QWEN3, batch, cache_len, device, torch.float32)
+    with torch.inference_mode():
+        h_ref = ref.prefill(x, keys_ref, values_ref, row_ids, positions, oq.oa.Segments.from_lengths(lengths),
+                            cos[positions], sin[positions])
+        segments = aq.Segments.from_lengths(lengths, device)
+        cos_d, sin_d = cos.to(device), sin.to(device)
+        pos_d = positions.to(device)
+        h = model.prefill(x.to(device), cache, row_ids.to(device), pos_d, segments, cos_d[pos_d], sin_d[pos_d])
+        assert max_rel_err(h.cpu(), h_ref) < 1e-4
+        assert max_rel_err(cache.keys.cpu(), keys_ref) < 1e-4
+
+        step_pos = torch.tensor([lengths[rows.index(r)] for r in range(batch)])
+        for step in range(5):
+            tokens = torch.randint(0, QWEN3["vocab_size"], (batch,), generator=g)
+            s_ref = ref.step(tokens, step_pos, keys_ref, values_ref, cos, sin)
+            s = model.step(tokens.to(device), step_pos.to(device), cache, cos_d, sin_d)
+            assert max_rel_err(s.cpu(), s_ref) < 1e-4, step
+            step_pos = step_pos + 1
+
+
+def test_qwen_step_mask_forms_agree(device):
+    """The reference's three step masks -- varlen tuple, boolean mask over a
+    shorter bucket view, KeyPrefix -- give the same attention."""
+    from asrback_amd import qwen3_asr as aq
+    from asrback_amd.attention import KeyPrefix
+
+    say("qwen3 mask forms")
+    torch.manual_seed(10)
+    attn = aq.TextAttention(QWEN3).to(device).eval()
+    batch = 4
+    keys = torch.randn(batch, 1024, 2, 128, device=device)
+    values = torch.randn(batch, 1024, 2, 128, device=device)
+    positions = torch.tensor([3, 100, 511, 255], device=device)
+    x = torch.randn(batch, QWEN3["hidden_size"], device=device)
+    cos, sin = aq.rope_tables(QWEN3, 1024, device, torch.float32)
+    cos, sin = cos[positions], sin[positions]
+    lengths = (positions + 1).to(torch.int32)
+    starts = torch.arange(batch + 1, dtype=torch.int32, device=device)
+    with torch.inference_mode():
+        a = attn.step(x, keys.clone(), values.clone(), positions, (starts, starts * 1024, lengths), cos, sin)
+        mask = oa.qwen_step_mask(positions, 512)
+        b = attn.step(x, keys.clone()[:, :512], values.clone()[:, :512], positions, mask, cos, sin)
+        c = attn.step(x, keys.clone(), values.clone(), positions, KeyPrefix(lengths=lengths), cos, sin)
+    assert max_rel_err(b, a) < 1e-6
+    assert torch.equal(a, c)
+
+
+def test_qwen_step_replays_from_graph(device):
+    """The decoder step of TextModel captured in a hipGraph and replayed at
+    advancing positions matches eager steps."""
+    from asrback_amd import qwen3_asr as aq
+    from asrback_amd.transcription import CapturedGraph
+
+    say("qwen3 graph replay")
+    _, model = qwen_pair(device)
+    batch = 4
+    cache = aq.KVCache.allocate(QWEN3, batch, 256, device, torch.float32)
+    torch.nn.init.normal_(cache.keys)
+    torch.nn.init.normal_(cache.values)
+    snapshot = (cache.keys.clone(), cache.values.clone())
+    cos, sin = aq.rope_tables(QWEN3, 256, device, torch.float32)
+    tokens = torch.tensor([1, 2, 3, 4], device=device)
+    positions = torch.tensor([10, 50, 0, 200], device=device)
+    out = torch.empty(batch, QWEN3["hidden_size"], device=device)
+
+    def step():
+        out.copy_(model.step(tokens, positions, cache, cos, sin))
+        positions.add_(1)
+
+    with torch.inference_mode():
+        graph = CapturedGraph(step)
+        # Reset after warm-up and capture, then replay 3 steps.
+        cache.keys.copy_(snapshot[0])
+        cache.values.copy_(snapshot[1])
+        positions.copy_(torch.tensor([10, 50, 0, 200]))
+        replayed = []
+        for _ in range(3):
+            graph.replay()
+            torch.cuda.synchronize()
+            replayed.append(out.clone())
+        cache.keys.copy_(snapshot[0])
+        cache.values.copy_(snapshot[1])
+        pos = torch.tensor([10, 50, 0, 200], device=device)
+        for i in range(3):
+            eager = model.step(tokens, pos, cache, cos, sin)
+            assert torch.equal(eager, replayed[i]), i
+            pos = pos + 1
+
+
+def test_qwen_audio_attention_windows(device):
+    """Windowed non-causal audio attention, 16 heads x 64 (qwen3_asr.py:207-221, :303-310)."""
+    from asrback_amd import qwen3_asr as aq
+
+    say("qwen3 audio windows")
+    ref = oq.AudioAttention(1024, 16).eval()
+    state = named_weights(ref, 11)
+    ref.load_state_dict(state)
+    model = aq.AudioAttention(1024, 16)
+    model.load_state_dict(state, strict=True)
+    model = model.eval().to(device)
+    lengths = [104, 104, 37, 81]
+    g = torch.Generator().manual_seed(12)
+    x = torch.randn(sum(lengths), 1024, generator=g)
+    with torch.inference_mode():
+        expected = ref(x, oa.Segments.from_lengths(lengths))
+        out = model(x.to(device), aq.Segments.from_lengths(lengths, device))
+    assert max_rel_err(out.cpu(), expected) < 1e-4

@@ -1,0 +1,112 @@
+"""CPU: host-side logic of the attention wrappers -- argument handling, mask
+conversion and error mapping -- without launching kernels.
+
+Failure injection follows the reference's own tests (host-side monkeypatching,
+``tests/test_models.py:36-45``): a nonzero C-ABI status must surface as a
+Python ``RuntimeError`` carrying the library's message.
+"""
+
+from __future__ import annotations
+
+import subprocess
+import sys
+
+import pytest
+import torch
+
+from conftest import ROOT
+
+
+def test_key_prefix_validation_and_mask_conversion():
+    from asrback_amd.attention import KeyPrefix
+
+    with pytest.raises(ValueError):
+        KeyPrefix()
+    with pytest.raises(ValueError):
+        KeyPrefix(positions=torch.zeros(2, dtype=torch.int64), lengths=torch.zeros(2, dtype=torch.int32))
+    with pytest.raises(TypeError):
+        KeyPrefix(positions=torch.zeros(2, dtype=torch.int32))
+    mask = torch.arange(10)[None, :] <= torch.tensor([0, 4, 9])[:, None]  # whisper.py:263-264
+    prefix = KeyPrefix.from_mask(mask[:, None, None, :])
+    assert prefix.lengths.tolist() == [1, 5, 10]
+    with pytest.raises(TypeError):
+        KeyPrefix.from_mask(mask.float())
+
+
+def test_ops_refuse_cpu_tensors_instead_of_falling_back():
+    from asrback_amd import attention
+
+    q = torch.zeros(2, 4, 64)
+    k = torch.zeros(2, 8, 4, 64)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        attention.decode(q, k, k)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        attention.flash(q[:, None], k, k)
+    with pytest.raises(TypeError, match="float32 and bfloat16"):
+        attention.decode(q.half(), k.half(), k.half())
+
+
+def test_shape_errors_are_reported():
+    from asrback_amd import attention
+
+    with pytest.raises(ValueError):
+        attention.decode(torch.zeros(2, 4, 64), torch.zeros(2, 8, 3, 64), torch.zeros(2, 8, 3, 64))
+    with pytest.raises(ValueError, match="window_size"):
+        attention.varlen_attn(torch.zeros(4, 2, 64), torch.zeros(4, 2, 64), torch.zeros(4, 2, 64),
+                              torch.zeros(2, dtype=torch.int32), torch.zeros(2, dtype=torch.int32), 4, 4,
+                              window_size=(8, 8))
+
+
+def test_nonzero_status_raises_runtime_error(monkeypatch):
+    from asrback_amd import _lib
+
+    class FakeLib:
+        def asrattn_last_error(self):
+            return b"no decode kernel for head_dim 96"
+
+    monkeypatch.setattr(_lib, "_handle", FakeLib())
+    with pytest.raises(RuntimeError, match="head_dim 96") as info:
+        _lib.check(_lib.ERR_UNSUPPORTED, "asrattn_decode")
+    assert isinstance(info.value, _lib.AttentionError)
+    assert info.value.status == _lib.ERR_UNSUPPORTED
+    _lib.check(_lib.OK, "asrattn_decode")  # no exception
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    from asrback_amd import _lib
+
+    monkeypatch.setattr(_lib, "_handle", None)
+    monkeypatch.setattr(_lib, "LIBRARY", tmp_path / "libasrattn.so")
+    with pytest.raises(RuntimeError, match="not built"):
+        _lib.load()
+
+
+def test_qwen_step_lengths_from_every_mask_form():
+    from asrback_amd.attention import KeyPrefix
+    from asrback_amd.qwen3_asr import _step_lengths
+    from oracle import attention as oa
+
+    positions = torch.tensor([0, 7, 300])
+    lengths = torch.tensor([1, 8, 301], dtype=torch.int32)
+    starts = torch.arange(4, dtype=torch.int32)
+    assert torch.equal(_step_lengths((starts, starts * 1024, lengths), positions, 1024), lengths)
+    assert torch.equal(_step_lengths(oa.qwen_step_mask(positions, 512), positions, 512), lengths)
+    assert torch.equal(_step_lengths(KeyPrefix(positions=positions), positions, 1024), lengths)
+    assert _step_lengths(None, positions, 256).tolist() == [1, 8, 256]
+
+
+def test_segments_from_lengths_on_cpu():
+    from asrback_amd.qwen3_asr import Segments
+
+    segments = Segments.from_lengths([3, 5, 2], torch.device("cpu"))
+    assert segments.starts.tolist() == [0, 3, 8, 10]
+    assert segments.starts.dtype == torch.int32
+    assert segments.longest == 5
+
+
+def test_bench_refuses_more_than_one_gpu():
+    result = subprocess.run(
+        [sys.executable, str(ROOT / "bench.py"), "--gpus", "8"], capture_output=True, text=True, timeout=120
+    )
+    assert result.returncode == 2
+    assert "one GPU" in result.stderr
