@@ -46,3 +46,25 @@ def test_step_attention_is_bucket_invariant():
     short = oa.sdpa(q, k[:, :, :64], v[:, :, :64], attn_mask=oa.whisper_step_mask(positions, 64))
     full = oa.sdpa(q, k, v, attn_mask=oa.whisper_step_mask(positions, 448))
     assert max_rel_err(short, full) < 1e-12
+
+
+def test_decoder_steps_equal_prompt_pass():
+    """Pins the oracle's decoder loop (cache writes, step mask, positions):
+    feeding a prompt one token at a time through the fixed-shape step path
+    (whisper.py:224-228, :260-264) gives the hidden states of the eager
+    causal prompt pass (whisper.py:229-237)."""
+    config = dict(ow.WHISPER_TINY, vocab_size=600, decoder_layers=2, encoder_layers=1)
+    model = ow.WhisperForConditionalGeneration(config).double().eval()
+    model.load_state_dict({k: v.double() for k, v in ow.named_weights(model, 3).items()})
+    g = torch.Generator().manual_seed(4)
+    encoded = torch.randn(2, 1500, 384, generator=g, dtype=torch.float64)
+    tokens = torch.randint(0, 600, (2, 6), generator=g)
+    with torch.inference_mode():
+        cache = model.allocate_cache(2, torch.float64)
+        model.set_encoder_output(cache, encoded)
+        full = model.model.decoder(tokens, torch.arange(6), cache, 6)
+        cache = model.allocate_cache(2, torch.float64)
+        model.set_encoder_output(cache, encoded)
+        for p in range(6):
+            step = model.model.decoder(tokens[:, p : p + 1], torch.full((2,), p), cache, None)
+            assert max_rel_err(step[:, 0], full[:, p]) < 1e-10, p
