@@ -412,6 +412,54 @@ def cpu_baseline(budget_s: float = 10.0) -> dict:
     }
 
 
+def shape_sweep(torch, attention) -> None:
+    """Average launch time of the encoder kernel over shapes: where its time
+    goes (fixed cost per launch, per-sequence critical path, throughput)."""
+
+    def launch_us(fn, reps=20):
+        stream = torch.cuda.Stream()
+        stream.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(stream):
+            fn()
+        torch.cuda.current_stream().wait_stream(stream)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(reps):
+                fn()
+        graph.replay()
+        torch.cuda.synchronize()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(5):
+            graph.replay()
+        stop.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(stop) * 1e3 / (5 * reps)
+
+    rng = np.random.default_rng(1)
+    ragged = list((rng.integers(100, 501, size=32) + 4).astype(int))
+    cases = [
+        ("SenseVoice ragged B=32 (headline)", 32, 4, max(ragged), 128, ragged),
+        ("uniform B=32 L=504", 32, 4, 504, 128, None),
+        ("uniform B=32 L=128", 32, 4, 128, 128, None),
+        ("uniform B=128 L=504", 128, 4, 504, 128, None),
+        ("uniform B=8 L=504", 8, 4, 504, 128, None),
+        ("one 64-row tile, 64 keys", 1, 1, 64, 128, None),
+        ("B=4 H=16 L=4096 hd=128", 4, 16, 4096, 128, None),
+        ("Whisper turbo B=16 H=20 L=1500 hd=64", 16, 20, 1500, 64, None),
+    ]
+    print("| Shape | us per launch | TFLOP/s |")
+    print("|---|---|---|")
+    for name, batch, heads, length, hd, lengths in cases:
+        q, k, v = (torch.randn(batch, length, heads, hd, device="cuda", dtype=torch.bfloat16) for _ in range(3))
+        used = None if lengths is None else torch.tensor(lengths, dtype=torch.int32, device="cuda")
+        out = torch.empty_like(q)
+        us = launch_us(lambda: attention.flash(q, k, v, seqused_k=used, out=out))
+        lens = lengths if lengths is not None else [length] * batch
+        flops = sum(4 * n * n * heads * hd for n in lens)
+        print(f"| {name} | {us:.2f} | {flops / us / 1e6:.1f} |", flush=True)
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     parser.add_argument("--gpus", type=int, default=1)
@@ -420,6 +468,8 @@ def main() -> int:
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--only", choices=["sensevoice", "turbo", "qwen3", "whisper-small", "copy"], default=None,
                         help="measure one workload only (for profiling)")
+    parser.add_argument("--sweep", action="store_true",
+                        help="time the encoder kernel over a table of shapes (one launch per line)")
     args = parser.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -438,6 +488,9 @@ def main() -> int:
         print("bench.py needs a GPU", file=sys.stderr)
         return 2
     torch.cuda.set_device(0)
+    if args.sweep:
+        shape_sweep(torch, attention)
+        return 0
     selected = {
         "sensevoice": SenseVoiceEncoder,
         "turbo": WhisperTurboEncoder,
