@@ -169,6 +169,11 @@ int asrattn_decode(const asrattn_decode_params* params, void* workspace, size_t 
       !vec_aligned(p.v, p.dtype, {p.v_batch_stride, p.v_token_stride, p.v_head_stride}))
     return fail(ASRATTN_ERR_INVALID,
                 "q, k and v need 16-byte aligned pointers and strides that are multiples of 16 bytes");
+  // Keys are addressed with 32-bit byte offsets from the sequence's start.
+  const long long es = p.dtype == ASRATTN_BF16 ? 2 : 4;
+  if ((long long)p.max_len_k * p.k_token_stride * es >= (1LL << 31) ||
+      (long long)p.max_len_k * p.v_token_stride * es >= (1LL << 31))
+    return fail(ASRATTN_ERR_UNSUPPORTED, "one sequence's keys span 2 GiB or more");
   const int s = decode_splits(p);
   const DecodeWorkspace w = decode_workspace(p, s);
   float* ws_o = nullptr;

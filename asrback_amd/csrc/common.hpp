@@ -63,19 +63,33 @@ struct Elem<bf16_raw> {
   static __device__ __forceinline__ void store1(bf16_raw* p, float x) { *p = f32_to_bf16(x); }
 };
 
-// Butterfly reductions inside aligned groups of W lanes (W a power of two
-// <= 64); every lane of the group ends with the result.
+// Butterfly sum inside aligned groups of W lanes (W a power of two <= 64);
+// every lane of the group ends with the group's sum.  Steps within 16 lanes
+// use DPP (quad permutes, then half-row and row mirrors, which pair equal
+// partial sums once the smaller groups are summed); wider steps use
+// ds_bpermute.
 template <int W>
 __device__ __forceinline__ float group_sum(float x) {
+  if constexpr (W >= 2) x += __builtin_amdgcn_update_dpp(0.f, x, 0xB1, 0xF, 0xF, false);   // quad_perm [1,0,3,2]
+  if constexpr (W >= 4) x += __builtin_amdgcn_update_dpp(0.f, x, 0x4E, 0xF, 0xF, false);   // quad_perm [2,3,0,1]
+  if constexpr (W >= 8) x += __builtin_amdgcn_update_dpp(0.f, x, 0x141, 0xF, 0xF, false);  // row_half_mirror
+  if constexpr (W >= 16) x += __builtin_amdgcn_update_dpp(0.f, x, 0x140, 0xF, 0xF, false); // row_mirror
 #pragma unroll
-  for (int off = W / 2; off > 0; off >>= 1) x += __shfl_xor(x, off, 64);
+  for (int off = 16; off < W; off <<= 1) x += __shfl_xor(x, off, 64);
   return x;
 }
-template <int W>
-__device__ __forceinline__ float group_max(float x) {
-#pragma unroll
-  for (int off = W / 2; off > 0; off >>= 1) x = fmaxf(x, __shfl_xor(x, off, 64));
-  return x;
+
+// Raw buffer resource over [base, base + bytes): 16-byte loads past the end
+// return zeros, so guarded loads need no branch.  base must be uniform over
+// the wave.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+
+__device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t rsrc, uint32_t voffset, uint32_t soffset = 0) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, voffset, soffset, 0);
+  return make_uint4(v[0], v[1], v[2], v[3]);
 }
 
 // Keys sequence b uses in a decoder step: seqused_k, else positions + 1,

@@ -23,8 +23,8 @@
 //     partial, so the grid depends only on shapes and the launch can be
 //     replayed from a graph while lengths change.
 //
-// Softmax runs in base 2: q is pre-multiplied by scale * log2(e), so
-// p = 2^(s - max) on v_exp_f32.
+// Softmax runs in base 2: each reduced score q . k is multiplied by
+// scale * log2(e), so p = 2^(s - max) on v_exp_f32.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -39,17 +39,45 @@ struct DecodeArgs {
   float c;  // scale * log2(e)
 };
 
-template <typename T, int HD, int W>
+template <typename T, int HD, int G, int W>
 struct DecodeShape {
   static constexpr int kEPL = Elem<T>::kPerVec;   // elements per lane per load
   static constexpr int kLPK = HD / kEPL;          // lanes per key row
   static constexpr int kKPW = 64 / kLPK;          // key rows per wave load (streams per wave)
   static constexpr int kThreads = 64 * W;
   static constexpr int kStreams = W * kKPW;       // softmax streams per workgroup
-  static constexpr int kUnroll = 4;               // keys per stream per load batch
+  // Keys per stream per load batch; with four query heads per kv head the
+  // batches are halved so that two of them fit beside the heads' state in
+  // 128 VGPRs.
+  static constexpr int kUnroll = G >= 4 ? 2 : 4;
   static constexpr int kStep = kStreams * kUnroll;  // keys per load batch
   static_assert(kLPK >= 1 && kLPK <= 64 && (64 % kLPK) == 0, "head_dim/lane mapping");
 };
+
+// q . k over one lane's 16-byte slices, accumulated in fp32.
+template <typename T>
+__device__ __forceinline__ float dot16(const uint4& q, const uint4& k);
+
+template <>
+__device__ __forceinline__ float dot16<float>(const uint4& q, const uint4& k) {
+  float acc = __uint_as_float(q.x) * __uint_as_float(k.x);
+  acc = fmaf(__uint_as_float(q.y), __uint_as_float(k.y), acc);
+  acc = fmaf(__uint_as_float(q.z), __uint_as_float(k.z), acc);
+  return fmaf(__uint_as_float(q.w), __uint_as_float(k.w), acc);
+}
+
+// bf16 pairs on v_dot2c_f32_bf16: the products of two bf16 values are exact
+// in fp32, so this equals the unpacked fp32 dot product up to summation
+// order.
+template <>
+__device__ __forceinline__ float dot16<bf16_raw>(const uint4& q, const uint4& k) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  auto pair = [](uint32_t x) { return __builtin_bit_cast(bf16x2_t, x); };
+  float acc = __builtin_amdgcn_fdot2_f32_bf16(pair(q.x), pair(k.x), 0.f, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(pair(q.y), pair(k.y), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(pair(q.z), pair(k.z), acc, false);
+  return __builtin_amdgcn_fdot2_f32_bf16(pair(q.w), pair(k.w), acc, false);
+}
 
 template <typename T>
 __device__ __forceinline__ void unpack(const uint4& r, float* out);
@@ -71,9 +99,10 @@ __device__ __forceinline__ void unpack<bf16_raw>(const uint4& r, float* out) {
 // Online-softmax state of one stream for the G query heads of a kv head.
 template <typename T, int HD, int G, int W>
 struct Stream {
-  using S = DecodeShape<T, HD, W>;
+  using S = DecodeShape<T, HD, G, W>;
   static constexpr int EPL = S::kEPL;
-  float q[G][EPL];
+  uint4 q[G];   // the lane's raw 16-byte slice of each query head
+  float c;      // scale * log2(e), applied to the reduced score
   float m[G], l[G], o[G][EPL];
 
   __device__ __forceinline__ void init() {
@@ -93,15 +122,10 @@ struct Stream {
     float s[U][G];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      float kf[EPL];
-      unpack<T>(kr[u], kf);
 #pragma unroll
       for (int g = 0; g < G; ++g) {
-        float acc = 0.f;
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) acc = fmaf(q[g][e], kf[e], acc);
-        acc = group_sum<S::kLPK>(acc);
-        s[u][g] = (valid_mask >> u) & 1u ? acc : kNegInf;
+        const float acc = group_sum<S::kLPK>(dot16<T>(q[g], kr[u]));
+        s[u][g] = (valid_mask >> u) & 1u ? acc * c : kNegInf;
       }
     }
     float mu[G];
@@ -154,9 +178,11 @@ struct Stream {
   }
 };
 
+// At most 128 VGPRs, so that four waves fit per SIMD (two 8-wave workgroups
+// per CU).
 template <typename T, int HD, int G, int W>
-__global__ __launch_bounds__(64 * W) void decode_kernel(const DecodeArgs a) {
-  using S = DecodeShape<T, HD, W>;
+__global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeArgs a) {
+  using S = DecodeShape<T, HD, G, W>;
   constexpr int EPL = S::kEPL, LPK = S::kLPK, NS = S::kStreams, U = S::kUnroll, STEP = S::kStep;
   const asrattn_decode_params& p = a.p;
 
@@ -173,23 +199,30 @@ __global__ __launch_bounds__(64 * W) void decode_kernel(const DecodeArgs a) {
   const int k0 = min(n, split * chunk);
   const int k1 = min(n, k0 + chunk);
 
+  // q is used raw (no unpacking), so its load latency overlaps the first
+  // K/V batch's.
   Stream<T, HD, G, W> st;
   {
     const T* qp = static_cast<const T*>(p.q) + (int64_t)b * p.q_batch_stride +
                   (int64_t)hkv * G * p.q_head_stride + sub * EPL;
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      unpack<T>(*reinterpret_cast<const uint4*>(qp + (int64_t)g * p.q_head_stride), st.q[g]);
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) st.q[g][e] *= a.c;
-    }
+    for (int g = 0; g < G; ++g) st.q[g] = *reinterpret_cast<const uint4*>(qp + (int64_t)g * p.q_head_stride);
   }
+  st.c = a.c;
   st.init();
 
-  const T* kp = static_cast<const T*>(p.k) + (int64_t)b * p.k_batch_stride +
-                (int64_t)hkv * p.k_head_stride + sub * EPL;
-  const T* vp = static_cast<const T*>(p.v) + (int64_t)b * p.v_batch_stride +
-                (int64_t)hkv * p.v_head_stride + sub * EPL;
+  // K and V of this (sequence, kv head) through buffer resources that end
+  // at the split's last key: loads past it return zeros without a branch,
+  // so the two load batches stay in flight across the loop.
+  const char* kbase = reinterpret_cast<const char*>(static_cast<const T*>(p.k) + (int64_t)b * p.k_batch_stride +
+                                                    (int64_t)hkv * p.k_head_stride);
+  const char* vbase = reinterpret_cast<const char*>(static_cast<const T*>(p.v) + (int64_t)b * p.v_batch_stride +
+                                                    (int64_t)hkv * p.v_head_stride);
+  const uint32_t kts = (uint32_t)(p.k_token_stride * (int64_t)sizeof(T));
+  const uint32_t vts = (uint32_t)(p.v_token_stride * (int64_t)sizeof(T));
+  const __amdgpu_buffer_rsrc_t krs = buffer_rsrc(kbase, (uint32_t)k1 * kts);
+  const __amdgpu_buffer_rsrc_t vrs = buffer_rsrc(vbase, (uint32_t)k1 * vts);
+  const uint32_t lane_bytes = sub * EPL * (uint32_t)sizeof(T);
 
   // Key u of the batch starting at `base` is base + u * NS + stream.
   auto load = [&](uint4* kr, uint4* vr, int base) -> unsigned {
@@ -197,28 +230,25 @@ __global__ __launch_bounds__(64 * W) void decode_kernel(const DecodeArgs a) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int j = base + u * NS + stream;
-      if (j < k1) {
-        kr[u] = *reinterpret_cast<const uint4*>(kp + (int64_t)j * p.k_token_stride);
-        vr[u] = *reinterpret_cast<const uint4*>(vp + (int64_t)j * p.v_token_stride);
-        mask |= 1u << u;
-      } else {
-        kr[u] = make_uint4(0, 0, 0, 0);
-        vr[u] = make_uint4(0, 0, 0, 0);
-      }
+      kr[u] = buffer_load16(krs, (uint32_t)j * kts + lane_bytes);
+      vr[u] = buffer_load16(vrs, (uint32_t)j * vts + lane_bytes);
+      mask |= (j < k1 ? 1u : 0u) << u;
     }
     return mask;
   };
 
   // Two register batches in ping-pong: the next batch is in flight while the
   // current one is consumed.
+  // The first batch is issued unconditionally: with k0 >= k1 its offsets all
+  // lie past the resource's end and read zeros.
   uint4 ka[U], va[U], kb[U], vb[U];
-  unsigned ma = 0, mb = 0;
-  if (k0 < k1) ma = load(ka, va, k0);
+  unsigned mb = 0;
+  unsigned ma = load(ka, va, k0);
   for (int base = k0; base < k1; base += 2 * STEP) {
-    if (base + STEP < k1) mb = load(kb, vb, base + STEP);
+    mb = load(kb, vb, base + STEP);
     st.consume(ka, va, ma);
     if (base + STEP >= k1) break;
-    if (base + 2 * STEP < k1) ma = load(ka, va, base + 2 * STEP);
+    ma = load(ka, va, base + 2 * STEP);
     st.consume(kb, vb, mb);
   }
 

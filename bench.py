@@ -158,7 +158,7 @@ class Qwen3Decode(Workload):
     name = "qwen3-asr-1.7b-decode-attention"
     unit = "GB/s"
     bound = "hbm"
-    kernel = "decode_split_kernel"
+    kernel = "decode_kernel"
 
     def __init__(self, torch, attention, seed: int = 3, steps: int = 128) -> None:
         rng = np.random.default_rng(seed)
@@ -211,7 +211,7 @@ class WhisperSmallDecoderStep(Workload):
     name = "whisper-small-decoder-step-attention"
     unit = "GB/s"
     bound = "hbm"
-    kernel = "decode_split_kernel"
+    kernel = "decode_kernel"
 
     def __init__(self, torch, attention, seed: int = 4) -> None:
         rng = np.random.default_rng(seed)
