@@ -143,8 +143,8 @@ int asrattn_fwd(const asrattn_fwd_params* params, void* stream) {
     return fail(ASRATTN_ERR_INVALID,
                 "q, k, v and out need 16-byte aligned pointers and strides that are multiples of 16 bytes");
   const bool generic = (p.flags & ASRATTN_FWD_FORCE_VALU) != 0;
-  if (!generic && asrattn::fwd_mfma_supported(p.dtype, p.head_dim))
-    return from_hip(asrattn::launch_fwd_mfma(p, static_cast<hipStream_t>(stream)), "asrattn_fwd (mfma)");
+  if (!generic && asrattn::fwd_ring_supported(p))
+    return from_hip(asrattn::launch_fwd_ring(p, static_cast<hipStream_t>(stream)), "asrattn_fwd (ring)");
   if (asrattn::fwd_valu_supported(p.dtype, p.head_dim))
     return from_hip(asrattn::launch_fwd_valu(p, static_cast<hipStream_t>(stream)), "asrattn_fwd (valu)");
   return fail(ASRATTN_ERR_UNSUPPORTED, "no forward kernel for head_dim %d (supported: 64, 128)", p.head_dim);

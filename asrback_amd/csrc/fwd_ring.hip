@@ -1,0 +1,469 @@
+// Multi-row attention on the gfx950 matrix cores (bf16 operands, fp32
+// accumulation, v_mfma_f32_32x32x16_bf16) with K/V tiles streamed into an LDS
+// ring by DMA.
+//
+// Workgroup: W waves, each owning 32 query rows of one (sequence, head); the
+// waves share BN-key K and V tiles.  Tiles move from HBM straight into LDS
+// with buffer_load_dwordx4 ... lds (no register staging): ST ring stages keep
+// ST - 1 tiles in flight, and one barrier per tile separates "stage landed
+// for everyone" from "stage free for the next DMA".  The buffer resources end
+// at the workgroup's last visible key, so DMA lanes past it write zeros and
+// the last tile needs no guard.
+//
+// Per wave and tile the arithmetic is the transposed product, which keeps
+// everything a query row needs in one lane:
+//
+//   S^T = K . Q^T   A = K rows (LDS), B = Q^T (registers, loaded once).  The
+//                   32x32 result puts query row (lane % 32) in the lane and
+//                   16 keys in its accumulators; the half waves hold disjoint
+//                   keys of the same rows.
+//   O^T = V^T . P^T A = V^T read from the row-major V tile with the gfx950
+//                   transpose load (ds_read_b64_tr_b16), B = P^T taken
+//                   straight from the S^T accumulators: the MFMA sums its 16
+//                   k slots in any order, so one key order serves both
+//                   operands and P never moves between lanes.
+//
+// Softmax runs in base 2 with scale * log2(e) folded into one FMA per score;
+// the output is rescaled only when some row's running max moved.
+//
+// LDS layout: the DMA writes 64 consecutive 16-byte chunks per instruction,
+// so rows cannot be padded; instead the chunk order inside each row is
+// permuted (each lane fetches the global chunk that belongs in its slot):
+//   K: chunk c of row r sits at (c + r) mod 16 (head_dim 128) or
+//      (c + r / 2) mod 8 (head_dim 64), so the 16 rows one b128 operand read
+//      touches per cycle hit 16 different bank groups;
+//   V: chunk c of row r sits at c ^ 4 (r mod 4) (128) or c ^ 4 ((r / 2) mod 2)
+//      (64), so the four rows of a transpose read land in four different
+//      64-byte bank ranges.
+//
+// Work mapping: a flat grid of (sequence, head, query tile) items; ids are
+// remapped so that the ids dispatched to one XCD (i, i + 8, ...) are
+// consecutive items, keeping the query tiles of one (sequence, head) -- and
+// its K/V -- on one XCD's L2.
+#include "common.hpp"
+#include "fwd_common.hpp"
+#include "kernels.hpp"
+
+namespace asrattn {
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef short short4_t __attribute__((ext_vector_type(4)));
+typedef short short8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) short4_t* lds_short4_ptr;
+typedef __attribute__((address_space(3))) const bf16x8_t* lds_bf16x8_ptr;
+
+__device__ __forceinline__ f32x16_t mfma32(const bf16x8_t& a, const bf16x8_t& b, const f32x16_t& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// LDS reads by byte address, so that constant parts of an address fold
+// into the instruction's offset field.
+__device__ __forceinline__ bf16x8_t lds_read16(uint32_t addr) { return *(lds_bf16x8_ptr)(size_t)addr; }
+
+// Transpose load of 4 bf16: within each 16-lane group, lane j receives
+// element (j % 4) of the 8-byte chunks addressed by lanes 4k + j / 4,
+// k = 0..3.
+__device__ __forceinline__ short4_t ds_read_tr(uint32_t addr) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_ptr)(size_t)addr);
+}
+
+// One DMA instruction: lane i copies the 16 bytes at buffer offset `voff`
+// into LDS bytes [lds_base + 16 i, +16).  Issued as inline assembly so that
+// the compiler's wait-count pass, which cannot tell ring stages apart, does
+// not drain every DMA before each LDS read; the kernel waits for them itself
+// (wait_dma).  M0 is saved and restored around the instruction.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, uint32_t lds_base, uint32_t voff) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %2, %3, 0 offen lds\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(lds_base), "v"(voff), "s"(rsrc)
+      : "memory");
+}
+
+// s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt in bits 3:0 and 15:14; expcnt
+// and lgkmcnt left at their maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// Waits until at most `ahead` tiles' DMAs (PER instructions each) of this
+// wave are outstanding.
+template <int PER, int MAXAHEAD>
+__device__ __forceinline__ void wait_dma(int ahead) {
+  static_assert(MAXAHEAD <= 2, "ring depth");
+  if (MAXAHEAD >= 2 && ahead >= 2) {
+    wait_vmcnt<2 * PER>();
+  } else if (MAXAHEAD >= 1 && ahead >= 1) {
+    wait_vmcnt<PER>();
+  } else {
+    wait_vmcnt<0>();
+  }
+}
+
+// Id -> work item such that the ids one XCD receives (round-robin dispatch
+// over 8 XCDs) map to a contiguous range of items.
+__device__ __forceinline__ int xcd_remap(int id, int total) {
+  const int per = total / 8;
+  const int rem = total % 8;
+  const int x = id % 8;
+  const int k = id / 8;
+  return x * per + min(x, rem) + k;
+}
+
+template <int HD, int W, int BN, int ST>
+struct RingShape {
+  static constexpr int kBM = 32 * W;                  // query rows per workgroup
+  static constexpr int kThreads = 64 * W;
+  static constexpr int kKB = BN / 32;                 // 32-key blocks per tile
+  static constexpr int kKSteps = HD / 16;             // k-steps of S^T
+  static constexpr int kDB = HD / 32;                 // 32-row blocks of O^T
+  static constexpr int kRowBytes = HD * 2;
+  static constexpr int kCPR = HD / 8;                 // 16-byte chunks per row
+  static constexpr int kTileBytes = BN * kRowBytes;   // one K or V tile
+  static constexpr int kStageBytes = 2 * kTileBytes;  // K tile, then V tile
+  static constexpr int kDmaPerTile = BN * kCPR / 64;  // DMA instructions per K (or V) tile
+  static constexpr int kDmaPerWave = kDmaPerTile / W;
+  static constexpr int kOutRow = HD + 8;              // staged output row stride (elements)
+  static constexpr int kOutBytes = W * 32 * kOutRow * 2;
+  static constexpr int kRingBytes = ST * kStageBytes;
+  static constexpr int kLds = kRingBytes > kOutBytes ? kRingBytes : kOutBytes;
+  static_assert(HD == 64 || HD == 128, "head_dim");
+  static_assert(BN % 32 == 0 && kDmaPerTile % W == 0 && kDmaPerWave >= 1, "tile / workgroup mapping");
+  static_assert(ST >= 2 && ST <= 4, "ring depth");
+};
+
+// Physical chunk of logical chunk c in row r of a K tile, and its inverse.
+template <int HD>
+__device__ __forceinline__ int k_phys(int r, int c) {
+  return HD == 128 ? ((c + r) & 15) : ((c + (r >> 1)) & 7);
+}
+template <int HD>
+__device__ __forceinline__ int k_logical(int r, int pc) {
+  return HD == 128 ? ((pc - r) & 15) : ((pc - (r >> 1)) & 7);
+}
+// V tiles: an XOR, its own inverse.
+template <int HD>
+__device__ __forceinline__ int v_phys(int r, int c) {
+  return HD == 128 ? (c ^ (4 * (r & 3))) : (c ^ (4 * ((r >> 1) & 1)));
+}
+
+template <int HD, int W, int BN, int ST, int OCC>
+__global__ __launch_bounds__(64 * W, OCC) void fwd_ring_kernel(const FwdArgs a, int q_tiles, int total) {
+  using S = RingShape<HD, W, BN, ST>;
+  constexpr int BM = S::kBM, KST = S::kKSteps, DB = S::kDB, KB = S::kKB, RBYTES = S::kRowBytes;
+  constexpr int CPR = S::kCPR, NPW = S::kDmaPerWave, SB = S::kStageBytes, TB = S::kTileBytes;
+  const asrattn_fwd_params& p = a.p;
+
+  const int item = xcd_remap(blockIdx.x, total);
+  const int qt = item % q_tiles;
+  const int bh = item / q_tiles;
+  const int hq = bh % p.heads_q;
+  const int b = bh / p.heads_q;
+  const int hkv = hq / (p.heads_q / p.heads_kv);
+  const SeqView sv = seq_view(p, b, hq, hkv);
+  const int row0 = qt * BM;
+  if (row0 >= sv.len_q) return;  // uniform over the workgroup
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: DMA destinations live in SGPRs
+  const int r32 = lane & 31;
+  const int half = lane >> 5;
+  const int wrow0 = row0 + 32 * wave;
+  const int row = wrow0 + r32;
+  const bool row_ok = row < sv.len_q;
+  const int row_lim = visible_keys(p, sv, row);
+  // Keys the workgroup (its last row) and this wave (its last row) see.
+  const int kend = visible_keys(p, sv, min(row0 + BM, sv.len_q) - 1);
+  const int wkend = wrow0 < sv.len_q ? visible_keys(p, sv, min(wrow0 + 32, sv.len_q) - 1) : 0;
+  const int n_tiles = (kend + BN - 1) / BN;
+
+  __shared__ __attribute__((aligned(16))) unsigned char lds[S::kLds];
+  // Low 32 bits of the flat address of an LDS variable are its LDS offset.
+  const uint32_t lds_base = (uint32_t)(uintptr_t)lds;
+
+  // Q^T operand: lane (row, half) holds head_dim [16 kk + 8 half, +8).
+  bf16x8_t qreg[KST];
+  {
+    const bf16_raw* qp = static_cast<const bf16_raw*>(p.q) + sv.q_off +
+                         (int64_t)(row_ok ? row : 0) * p.q_token_stride + half * 8;
+#pragma unroll
+    for (int kk = 0; kk < KST; ++kk) {
+      const uint4 v = row_ok ? *reinterpret_cast<const uint4*>(qp + kk * 16) : make_uint4(0, 0, 0, 0);
+      qreg[kk] = __builtin_bit_cast(bf16x8_t, v);
+    }
+  }
+
+  // K/V of the (sequence, kv head) up to the workgroup's last visible key.
+  const uint32_t kts = (uint32_t)(p.k_token_stride * 2);
+  const uint32_t vts = (uint32_t)(p.v_token_stride * 2);
+  const __amdgpu_buffer_rsrc_t krs =
+      buffer_rsrc(static_cast<const bf16_raw*>(p.k) + sv.k_off, (uint32_t)kend * kts);
+  const __amdgpu_buffer_rsrc_t vrs =
+      buffer_rsrc(static_cast<const bf16_raw*>(p.v) + sv.v_off, (uint32_t)kend * vts);
+
+  // DMA instruction wave * NPW + i of a tile fills LDS slots 64 j + lane:
+  // physical row s / CPR, physical chunk s % CPR, holding the logical chunk
+  // the permutation puts there.
+  uint32_t koff[NPW], voff[NPW];
+#pragma unroll
+  for (int i = 0; i < NPW; ++i) {
+    const int s = 64 * (wave * NPW + i) + lane;
+    const int pr = s / CPR;
+    const int pc = s % CPR;
+    koff[i] = (uint32_t)pr * kts + (uint32_t)k_logical<HD>(pr, pc) * 16;
+    voff[i] = (uint32_t)pr * vts + (uint32_t)v_phys<HD>(pr, pc) * 16;
+  }
+  // Tile t goes to ring stage t % ST (passed as `stage`, a constant after
+  // unrolling).
+  auto issue = [&](int t, int stage_idx) {
+    const uint32_t stage = lds_base + (uint32_t)stage_idx * SB;
+    const uint32_t kk0 = (uint32_t)(t * BN) * kts;
+    const uint32_t vv0 = (uint32_t)(t * BN) * vts;
+#pragma unroll
+    for (int i = 0; i < NPW; ++i)
+      dma16(krs, stage + (uint32_t)(wave * NPW + i) * 1024, koff[i] + kk0);
+#pragma unroll
+    for (int i = 0; i < NPW; ++i)
+      dma16(vrs, stage + TB + (uint32_t)(wave * NPW + i) * 1024, voff[i] + vv0);
+  };
+
+  // Operand addresses in stage 0.  K: row 32 kb + r32, logical chunk
+  // 2 kk + half.  V (transpose read): key row 16 t + 8 hi + tr_row and
+  // columns 32 db + tr_col of each 8-key x 32-column block.  The addresses
+  // are masked to 18 bits (LDS addresses), which proves their sign bit
+  // clear: only then do the constant parts added below (stage, key block,
+  // k-step) fold into the ds_read offset field.
+  uint32_t kaddr[KST];
+#pragma unroll
+  for (int kk = 0; kk < KST; ++kk)
+    kaddr[kk] = (lds_base + (uint32_t)r32 * RBYTES + (uint32_t)k_phys<HD>(r32, 2 * kk + half) * 16) & 0x3ffffu;
+  const int tr_row = 4 * ((lane >> 4) >> 1) + ((lane & 15) >> 2);
+  const int tr_cc = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);  // chunk within the 32-column block
+  uint32_t vaddr[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+    vaddr[db] = (lds_base + TB + (uint32_t)tr_row * RBYTES + (uint32_t)v_phys<HD>(tr_row, 4 * db + tr_cc) * 16 +
+                 (lane & 1) * 8) & 0x3ffffu;
+
+  f32x16_t oacc[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) oacc[db] = f32x16_t{};
+  const float c = a.c;
+  // Running row max in scaled (base-2) units, possibly stale by up to
+  // kLazy: scores are exponentiated against it, so p <= 2^kLazy, which fp32
+  // sums and bf16 operands hold with unchanged relative precision.  O and l
+  // are rescaled only when some row's max grows by more than that.
+  constexpr float kLazy = 8.f;
+  float m_run = kNegInf;
+  float l_run = 0.f;
+
+  // Tiles this wave computes (a prefix: causal rows see fewer keys), and
+  // whether tile j needs the per-key mask (some row of the wave sees fewer
+  // than all of its keys; the wave's first row sees the fewest).
+  const int wtiles = (wkend + BN - 1) / BN;
+  const int wmin = wrow0 < sv.len_q ? visible_keys(p, sv, wrow0) : 0;
+  auto masked = [&](int j) { return (j + 1) * BN > wmin; };
+
+  // S^T of tile j (stage stage_idx) into s.
+  auto qk = [&](int stage_idx, f32x16_t* s) {
+    const uint32_t so = (uint32_t)stage_idx * SB;
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) s[kb] = f32x16_t{};
+#pragma unroll
+    for (int kk = 0; kk < KST; ++kk) {
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) s[kb] = mfma32(lds_read16(kaddr[kk] + so + kb * 32 * RBYTES), qreg[kk], s[kb]);
+    }
+  };
+  // Keys at or past the row's limit -> -inf.  Accumulator r of block kb is
+  // key kt + 32 kb + 8 (r / 4) + 4 half + r % 4.
+  auto mask = [&](int kt, f32x16_t* s) {
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = kt + kb * 32 + (r / 4) * 8 + half * 4 + (r % 4);
+        if (key >= row_lim) s[kb][r] = kNegInf;
+      }
+  };
+  // Row max over the tile, combined across the half waves, scaled.
+  auto rowmax = [&](const f32x16_t* s) {
+    float mt = s[0][0];
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+      for (int r = (kb == 0 ? 1 : 0); r < 16; ++r) mt = fmaxf(mt, s[kb][r]);
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt), false, false);
+    return fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * c;
+  };
+  // P^T = 2^(s c - mu) as bf16 MFMA operands; returns the fp32 sum.
+  auto softmax = [&](const f32x16_t* s, float mu, bf16x8_t* pb) {
+    float psum = 0.f;
+#pragma unroll
+    for (int t = 0; t < 2 * KB; ++t) {
+      uint32_t w[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float p0 = fast_exp2(fmaf(s[t / 2][(t % 2) * 8 + 2 * i], c, -mu));
+        const float p1 = fast_exp2(fmaf(s[t / 2][(t % 2) * 8 + 2 * i + 1], c, -mu));
+        psum += p0 + p1;
+        w[i] = pack_bf16x2(p0, p1);
+      }
+      pb[t] = __builtin_bit_cast(bf16x8_t, make_uint4(w[0], w[1], w[2], w[3]));
+    }
+    return psum;
+  };
+  // O^T += V^T . P^T over tile stage stage_idx.  MFMA t covers keys
+  // 16 t + 8 (idx / 4) + 4 half + idx % 4.
+  auto pv = [&](int stage_idx, const bf16x8_t* pb) {
+    const uint32_t so = (uint32_t)stage_idx * SB;
+#pragma unroll
+    for (int t = 0; t < 2 * KB; ++t) {
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        const short4_t lo = ds_read_tr(vaddr[db] + so + 16 * t * RBYTES);
+        const short4_t hi = ds_read_tr(vaddr[db] + so + (16 * t + 8) * RBYTES);
+        const bf16x8_t av = __builtin_bit_cast(bf16x8_t, (short8_t){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
+        oacc[db] = mfma32(av, pb[t], oacc[db]);
+      }
+    }
+  };
+#pragma unroll
+  for (int t = 0; t < ST - 1; ++t)
+    if (t < n_tiles) issue(t, t);
+  // The compiler tracks the Q loads but not the DMAs; consuming Q here makes
+  // its wait for them happen once, before the loop, instead of before the
+  // first MFMA of every tile (where it would drain the ring).
+#pragma unroll
+  for (int kk = 0; kk < KST; ++kk) asm volatile("" ::"v"(qreg[kk]));
+
+  // Tile j (ring stage stage_idx = j % ST): S^T, mask, row max, lazy
+  // rescale, P^T and O^T += V^T P^T.
+  auto tile = [&](int j, int stage_idx) {
+    // This wave's part of tile j has landed once at most the tiles after it
+    // are outstanding; after the barrier every wave's part has, and every
+    // wave is done with tile j - 1, whose stage the next DMA reuses.
+    wait_dma<2 * NPW, ST - 2>(min(ST - 2, n_tiles - 1 - j));
+    __syncthreads();
+    if (j + ST - 1 < n_tiles) issue(j + ST - 1, (stage_idx + ST - 1) % ST);
+    if (j >= wtiles) return;  // uniform per wave; the barrier is above
+
+    f32x16_t s[KB];
+    qk(stage_idx, s);
+    if (masked(j)) mask(j * BN, s);
+    const float mt = rowmax(s);
+    // Rescale only when some row's max grew past the slack (always on the
+    // first tile, where m_run is -inf).
+    if (__any(mt > m_run + kLazy)) {
+      const float mn = fmaxf(m_run, mt);
+      const float alpha = mn == kNegInf ? 1.f : fast_exp2(m_run - mn);
+#pragma unroll
+      for (int db = 0; db < DB; ++db) oacc[db] *= alpha;
+      l_run *= alpha;
+      m_run = mn;
+    }
+    const float mu = m_run == kNegInf ? 0.f : m_run;
+    bf16x8_t pb[2 * KB];
+    l_run += softmax(s, mu, pb);
+    pv(stage_idx, pb);
+  };
+  // Unrolled over the ring so that every stage offset is a constant.
+  for (int j0 = 0; j0 < n_tiles; j0 += ST) {
+#pragma unroll
+    for (int st = 0; st < ST; ++st)
+      if (j0 + st < n_tiles) tile(j0 + st, st);
+  }
+  __syncthreads();  // the ring is free for the output staging
+  if (wrow0 >= sv.len_q) return;  // uniform per wave; no barrier follows
+
+  // The half waves hold disjoint keys of the same rows.
+  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  constexpr int ORS = S::kOutRow;
+  bf16_raw* const stage = reinterpret_cast<bf16_raw*>(lds) + wave * 32 * ORS;
+  // Accumulator r of block db is column 32 db + 8 (r / 4) + 4 half + r % 4
+  // of row r32: write the normalized rows to LDS ...
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t w0 = pack_bf16x2(oacc[db][4 * i] * inv, oacc[db][4 * i + 1] * inv);
+      const uint32_t w1 = pack_bf16x2(oacc[db][4 * i + 2] * inv, oacc[db][4 * i + 3] * inv);
+      *reinterpret_cast<uint2*>(stage + r32 * ORS + db * 32 + i * 8 + half * 4) = make_uint2(w0, w1);
+    }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  // ... and store them to global memory 16 bytes per lane, whole rows per
+  // instruction.
+  constexpr int kRowChunks = HD / 8;
+#pragma unroll
+  for (int i = 0; i < 32 * kRowChunks / 64; ++i) {
+    const int ch = i * 64 + lane;
+    const int r = ch / kRowChunks;
+    const int col = (ch % kRowChunks) * 8;
+    const int orow = wrow0 + r;
+    const uint4 val = *reinterpret_cast<const uint4*>(stage + r * ORS + col);
+    if (orow < sv.len_q) {
+      bf16_raw* op = static_cast<bf16_raw*>(p.out) + sv.o_off + (int64_t)orow * p.o_token_stride + col;
+      *reinterpret_cast<uint4*>(op) = val;
+    }
+  }
+}
+
+template <int HD, int W, int BN, int ST, int OCC>
+hipError_t launch_typed(const FwdArgs& a, hipStream_t stream) {
+  using S = RingShape<HD, W, BN, ST>;
+  const asrattn_fwd_params& p = a.p;
+  const int q_tiles = (p.max_len_q + S::kBM - 1) / S::kBM;
+  const long long total = (long long)q_tiles * p.heads_q * p.batch;
+  if (total <= 0) return hipSuccess;
+  if (total > 0x7fffffffLL) return hipErrorInvalidConfiguration;
+  hipLaunchKernelGGL((fwd_ring_kernel<HD, W, BN, ST, OCC>), dim3((unsigned)total), dim3(S::kThreads), 0, stream, a,
+                     q_tiles, (int)total);
+  return hipGetLastError();
+}
+
+template <int HD>
+hipError_t launch_hd(const FwdArgs& a, hipStream_t stream) {
+  // 64-key tiles.  Head dim 128 on sequences longer than 128 rows: eight
+  // waves (256 query rows) share each tile through three stages, one
+  // workgroup per CU.  Otherwise four waves (128 rows), two stages, two or
+  // more workgroups per CU whose waves pair up on the SIMDs without sharing a
+  // barrier.
+  if (HD == 128 && a.p.max_len_q > 128) return launch_typed<HD, 8, 64, 3, 2>(a, stream);
+  return launch_typed<HD, 4, 64, 2, 2>(a, stream);
+}
+
+}  // namespace
+
+bool fwd_ring_supported(const asrattn_fwd_params& p) {
+  if (p.dtype != ASRATTN_BF16 || (p.head_dim != 64 && p.head_dim != 128)) return false;
+  // A key row must end before the next one starts for the resource bound
+  // (last visible key's row end) to cover every visible key.
+  if (p.k_token_stride < p.head_dim || p.v_token_stride < p.head_dim) return false;
+  // K/V are addressed with 32-bit byte offsets from the sequence's first key,
+  // up to one tile past its last.
+  const long long span_k = ((long long)p.max_len_k + 256) * p.k_token_stride * 2;
+  const long long span_v = ((long long)p.max_len_k + 256) * p.v_token_stride * 2;
+  return span_k < (1LL << 31) && span_v < (1LL << 31);
+}
+
+hipError_t launch_fwd_ring(const asrattn_fwd_params& p, hipStream_t stream) {
+  FwdArgs a;
+  a.p = p;
+  a.c = p.scale * kLog2e;
+  return p.head_dim == 64 ? launch_hd<64>(a, stream) : launch_hd<128>(a, stream);
+}
+
+}  // namespace asrattn

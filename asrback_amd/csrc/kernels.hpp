@@ -17,12 +17,14 @@ hipError_t launch_decode(const asrattn_decode_params& p, int splits, float* ws_o
 int decode_waves(const asrattn_decode_params& p, int splits);
 bool decode_supported(int dtype, int head_dim, int group);
 
-// Multi-row forward on matrix cores (bf16, head_dim 64 or 128).
-hipError_t launch_fwd_mfma(const asrattn_fwd_params& p, hipStream_t stream);
-bool fwd_mfma_supported(int dtype, int head_dim);
+// Multi-row forward on matrix cores with K/V streamed into an LDS ring by
+// DMA (bf16, head_dim 64 or 128, K/V spans addressable with 32-bit offsets).
+hipError_t launch_fwd_ring(const asrattn_fwd_params& p, hipStream_t stream);
+bool fwd_ring_supported(const asrattn_fwd_params& p);
 
 // Multi-row forward on the vector ALUs (fp32 or bf16, head_dim 64 or 128):
-// the fp32 path and the reference-precision check of the matrix-core kernel.
+// the fp32 path, the fallback for bf16 layouts the matrix-core kernel does
+// not address, and the reference-precision check of that kernel.
 hipError_t launch_fwd_valu(const asrattn_fwd_params& p, hipStream_t stream);
 bool fwd_valu_supported(int dtype, int head_dim);
 

@@ -71,7 +71,7 @@ class SenseVoiceEncoder(Workload):
     name = "sensevoice-small-encoder-attention"
     unit = "TFLOP/s"
     bound = "mfma"
-    kernel = "fwd_mfma_kernel"
+    kernel = "fwd_ring_kernel"
 
     def __init__(self, torch, attention, seed: int = 1) -> None:
         rng = np.random.default_rng(seed)
@@ -122,7 +122,7 @@ class WhisperTurboEncoder(Workload):
     name = "whisper-large-v3-turbo-encoder-attention"
     unit = "TFLOP/s"
     bound = "mfma"
-    kernel = "fwd_mfma_kernel"
+    kernel = "fwd_ring_kernel"
 
     def __init__(self, torch, attention, seed: int = 2) -> None:
         self.batch, self.heads, self.head_dim, self.layers, self.length = 16, 20, 64, 32, 1500
