@@ -36,10 +36,12 @@
 //      (64), so the four rows of a transpose read land in four different
 //      64-byte bank ranges.
 //
-// Work mapping: a flat grid of (sequence, head, query tile) items; ids are
-// remapped so that the ids dispatched to one XCD (i, i + 8, ...) are
-// consecutive items, keeping the query tiles of one (sequence, head) -- and
-// its K/V -- on one XCD's L2.
+// Workgroups may also split the keys across waves (KS splits, merged through
+// LDS at the end), which shortens the longest workgroups of ragged batches.
+//
+// Work mapping: a flat grid of (sequence, head, query tile) items, taken
+// longest-first in ragged batches, with the query tiles of one (sequence,
+// head) -- and its K/V -- on one XCD's L2 (work_item).
 #include "common.hpp"
 #include "fwd_common.hpp"
 #include "kernels.hpp"
@@ -119,26 +121,85 @@ __device__ __forceinline__ int xcd_remap(int id, int total) {
   return x * per + min(x, rem) + k;
 }
 
-template <int HD, int W, int BN, int ST>
+// Workgroup of RB row blocks x KS key splits (one wave each); a ring stage
+// holds KS consecutive BN-key sub-tiles, split ks taking the ks-th.
+// Visible keys of sequence b before any causal limit.
+__device__ __forceinline__ int sequence_keys(const asrattn_fwd_params& p, int b) {
+  int n = p.cu_seqlens_k != nullptr ? p.cu_seqlens_k[b + 1] - p.cu_seqlens_k[b] : p.max_len_k;
+  n = min(max(n, 0), p.max_len_k);
+  if (p.seqused_k != nullptr) n = min(n, max(p.seqused_k[b], 0));
+  return n;
+}
+
+// The sequence of rank r in decreasing key count (ties in index order), for
+// batches of at most 64: lane b ranks sequence b against all others.
+__device__ __forceinline__ int ranked_sequence(const asrattn_fwd_params& p, int r) {
+  const int lane = threadIdx.x & 63;
+  const int n = lane < p.batch ? sequence_keys(p, lane) : -1;
+  int rank = 0;
+  for (int j = 0; j < p.batch; ++j) {
+    const int nj = __builtin_amdgcn_readlane(n, j);
+    rank += (nj > n || (nj == n && j < lane)) ? 1 : 0;
+  }
+  const unsigned long long hit = __ballot(lane < p.batch && rank == r);
+  return __ffsll(hit) - 1;  // ranks are a permutation: exactly one lane
+}
+
+// Launch id -> (sequence, query head, query tile).  Dispatch hands ids out
+// in order as workgroup slots free up, round-robin over the 8 XCDs.  With
+// per-sequence key counts (ragged batches of at most 64 sequences) the
+// (sequence, head) pairs are taken in decreasing key count -- the longest
+// work starts first and short pairs fill in behind it -- and pair P goes to
+// XCD P % 8 with its query tiles consecutive there, so its K/V stay in one
+// L2.  Otherwise ids are remapped so that each XCD gets a contiguous range of
+// items (the same L2 grouping).
+__device__ __forceinline__ void work_item(const asrattn_fwd_params& p, int q_tiles, int total, int& b, int& hq,
+                                          int& qt) {
+  const int id = blockIdx.x;
+  const bool ragged = p.seqused_k != nullptr || p.cu_seqlens_k != nullptr;
+  if (ragged && p.batch <= 64 && (p.batch * p.heads_q) % 8 == 0) {
+    const int k = id >> 3;
+    const int pair = (k / q_tiles) * 8 + (id & 7);
+    qt = k % q_tiles;
+    hq = pair % p.heads_q;
+    b = ranked_sequence(p, pair / p.heads_q);
+    return;
+  }
+  const int item = xcd_remap(id, total);
+  qt = item % q_tiles;
+  const int bh = item / q_tiles;
+  hq = bh % p.heads_q;
+  b = bh / p.heads_q;
+}
+
+template <int HD, int RB, int KS, int BN, int ST>
 struct RingShape {
-  static constexpr int kBM = 32 * W;                  // query rows per workgroup
-  static constexpr int kThreads = 64 * W;
-  static constexpr int kKB = BN / 32;                 // 32-key blocks per tile
+  static constexpr int kW = RB * KS;                  // waves
+  static constexpr int kBM = 32 * RB;                 // query rows per workgroup
+  static constexpr int kThreads = 64 * kW;
+  static constexpr int kSpan = KS * BN;               // keys per ring stage
+  static constexpr int kKB = BN / 32;                 // 32-key blocks per sub-tile
   static constexpr int kKSteps = HD / 16;             // k-steps of S^T
   static constexpr int kDB = HD / 32;                 // 32-row blocks of O^T
   static constexpr int kRowBytes = HD * 2;
   static constexpr int kCPR = HD / 8;                 // 16-byte chunks per row
-  static constexpr int kTileBytes = BN * kRowBytes;   // one K or V tile
-  static constexpr int kStageBytes = 2 * kTileBytes;  // K tile, then V tile
-  static constexpr int kDmaPerTile = BN * kCPR / 64;  // DMA instructions per K (or V) tile
-  static constexpr int kDmaPerWave = kDmaPerTile / W;
+  static constexpr int kTileBytes = kSpan * kRowBytes;  // the K (or V) rows of a stage
+  static constexpr int kStageBytes = 2 * kTileBytes;  // K rows, then V rows
+  static constexpr int kDmaPerTile = kSpan * kCPR / 64;  // DMA instructions per K (or V) rows of a stage
+  static constexpr int kDmaPerWave = kDmaPerTile / kW;
   static constexpr int kOutRow = HD + 8;              // staged output row stride (elements)
-  static constexpr int kOutBytes = W * 32 * kOutRow * 2;
+  static constexpr int kOutBytes = RB * 32 * kOutRow * 2;
+  // Key-split merge: per (row block, split > 0) the wave's O^T accumulators
+  // and (max, sum), lane-major floats.
+  static constexpr int kMergeFloats = (kDB * 16 + 2) * 64;
+  static constexpr int kMergeBytes = RB * (KS - 1) * kMergeFloats * 4;
   static constexpr int kRingBytes = ST * kStageBytes;
-  static constexpr int kLds = kRingBytes > kOutBytes ? kRingBytes : kOutBytes;
+  static constexpr int kEpilogue = KS > 1 ? kMergeBytes : kOutBytes;
+  static constexpr int kLds = kRingBytes > kEpilogue ? kRingBytes : kEpilogue;
   static_assert(HD == 64 || HD == 128, "head_dim");
-  static_assert(BN % 32 == 0 && kDmaPerTile % W == 0 && kDmaPerWave >= 1, "tile / workgroup mapping");
+  static_assert(BN % 32 == 0 && kDmaPerTile % kW == 0 && kDmaPerWave >= 1, "tile / workgroup mapping");
   static_assert(ST >= 2 && ST <= 4, "ring depth");
+  static_assert(KS == 1 || 32 * kOutRow * 2 <= kMergeFloats * 4, "output staging fits a merge slot");
 };
 
 // Physical chunk of logical chunk c in row r of a K tile, and its inverse.
@@ -156,18 +217,16 @@ __device__ __forceinline__ int v_phys(int r, int c) {
   return HD == 128 ? (c ^ (4 * (r & 3))) : (c ^ (4 * ((r >> 1) & 1)));
 }
 
-template <int HD, int W, int BN, int ST, int OCC>
-__global__ __launch_bounds__(64 * W, OCC) void fwd_ring_kernel(const FwdArgs a, int q_tiles, int total) {
-  using S = RingShape<HD, W, BN, ST>;
+template <int HD, int RB, int KS, int BN, int ST, int OCC>
+__global__ __launch_bounds__(64 * RB * KS, OCC) void fwd_ring_kernel(const FwdArgs a, int q_tiles, int total) {
+  using S = RingShape<HD, RB, KS, BN, ST>;
   constexpr int BM = S::kBM, KST = S::kKSteps, DB = S::kDB, KB = S::kKB, RBYTES = S::kRowBytes;
   constexpr int CPR = S::kCPR, NPW = S::kDmaPerWave, SB = S::kStageBytes, TB = S::kTileBytes;
+  constexpr int SPAN = S::kSpan;
   const asrattn_fwd_params& p = a.p;
 
-  const int item = xcd_remap(blockIdx.x, total);
-  const int qt = item % q_tiles;
-  const int bh = item / q_tiles;
-  const int hq = bh % p.heads_q;
-  const int b = bh / p.heads_q;
+  int b, hq, qt;
+  work_item(p, q_tiles, total, b, hq, qt);
   const int hkv = hq / (p.heads_q / p.heads_kv);
   const SeqView sv = seq_view(p, b, hq, hkv);
   const int row0 = qt * BM;
@@ -176,16 +235,18 @@ __global__ __launch_bounds__(64 * W, OCC) void fwd_ring_kernel(const FwdArgs a, 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: DMA destinations live in SGPRs
+  const int rb = wave % RB;  // row block
+  const int ks = wave / RB;  // key split
   const int r32 = lane & 31;
   const int half = lane >> 5;
-  const int wrow0 = row0 + 32 * wave;
+  const int wrow0 = row0 + 32 * rb;
   const int row = wrow0 + r32;
   const bool row_ok = row < sv.len_q;
   const int row_lim = visible_keys(p, sv, row);
   // Keys the workgroup (its last row) and this wave (its last row) see.
   const int kend = visible_keys(p, sv, min(row0 + BM, sv.len_q) - 1);
   const int wkend = wrow0 < sv.len_q ? visible_keys(p, sv, min(wrow0 + 32, sv.len_q) - 1) : 0;
-  const int n_tiles = (kend + BN - 1) / BN;
+  const int n_tiles = (kend + SPAN - 1) / SPAN;
 
   __shared__ __attribute__((aligned(16))) unsigned char lds[S::kLds];
   // Low 32 bits of the flat address of an LDS variable are its LDS offset.
@@ -227,8 +288,8 @@ __global__ __launch_bounds__(64 * W, OCC) void fwd_ring_kernel(const FwdArgs a, 
   // unrolling).
   auto issue = [&](int t, int stage_idx) {
     const uint32_t stage = lds_base + (uint32_t)stage_idx * SB;
-    const uint32_t kk0 = (uint32_t)(t * BN) * kts;
-    const uint32_t vv0 = (uint32_t)(t * BN) * vts;
+    const uint32_t kk0 = (uint32_t)(t * SPAN) * kts;
+    const uint32_t vv0 = (uint32_t)(t * SPAN) * vts;
 #pragma unroll
     for (int i = 0; i < NPW; ++i)
       dma16(krs, stage + (uint32_t)(wave * NPW + i) * 1024, koff[i] + kk0);
@@ -237,23 +298,27 @@ __global__ __launch_bounds__(64 * W, OCC) void fwd_ring_kernel(const FwdArgs a, 
       dma16(vrs, stage + TB + (uint32_t)(wave * NPW + i) * 1024, voff[i] + vv0);
   };
 
-  // Operand addresses in stage 0.  K: row 32 kb + r32, logical chunk
-  // 2 kk + half.  V (transpose read): key row 16 t + 8 hi + tr_row and
-  // columns 32 db + tr_col of each 8-key x 32-column block.  The addresses
+  // Operand addresses in stage 0, in this wave's sub-tile (rows ks BN ..).
+  // K: row 32 kb + r32, logical chunk 2 kk + half.  V (transpose read): key
+  // row 16 t + 8 hi + tr_row and columns 32 db + tr_col of each 8-key x
+  // 32-column block.  BN is a multiple of 32, so the chunk permutations
+  // depend on the same low row bits in every sub-tile.  The addresses
   // are masked to 18 bits (LDS addresses), which proves their sign bit
   // clear: only then do the constant parts added below (stage, key block,
   // k-step) fold into the ds_read offset field.
   uint32_t kaddr[KST];
 #pragma unroll
   for (int kk = 0; kk < KST; ++kk)
-    kaddr[kk] = (lds_base + (uint32_t)r32 * RBYTES + (uint32_t)k_phys<HD>(r32, 2 * kk + half) * 16) & 0x3ffffu;
+    kaddr[kk] = (lds_base + (uint32_t)(ks * BN + r32) * RBYTES + (uint32_t)k_phys<HD>(r32, 2 * kk + half) * 16) &
+                0x3ffffu;
   const int tr_row = 4 * ((lane >> 4) >> 1) + ((lane & 15) >> 2);
   const int tr_cc = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);  // chunk within the 32-column block
   uint32_t vaddr[DB];
 #pragma unroll
   for (int db = 0; db < DB; ++db)
-    vaddr[db] = (lds_base + TB + (uint32_t)tr_row * RBYTES + (uint32_t)v_phys<HD>(tr_row, 4 * db + tr_cc) * 16 +
-                 (lane & 1) * 8) & 0x3ffffu;
+    vaddr[db] = (lds_base + TB + (uint32_t)(ks * BN + tr_row) * RBYTES +
+                 (uint32_t)v_phys<HD>(tr_row, 4 * db + tr_cc) * 16 + (lane & 1) * 8) &
+                0x3ffffu;
 
   f32x16_t oacc[DB];
 #pragma unroll
@@ -267,12 +332,11 @@ __global__ __launch_bounds__(64 * W, OCC) void fwd_ring_kernel(const FwdArgs a, 
   float m_run = kNegInf;
   float l_run = 0.f;
 
-  // Tiles this wave computes (a prefix: causal rows see fewer keys), and
-  // whether tile j needs the per-key mask (some row of the wave sees fewer
-  // than all of its keys; the wave's first row sees the fewest).
-  const int wtiles = (wkend + BN - 1) / BN;
+  // Whether the sub-tile starting at key kt needs the per-key mask (some row
+  // of the wave sees fewer than all of its keys; the wave's first row sees
+  // the fewest).
   const int wmin = wrow0 < sv.len_q ? visible_keys(p, sv, wrow0) : 0;
-  auto masked = [&](int j) { return (j + 1) * BN > wmin; };
+  auto masked = [&](int kt) { return kt + BN > wmin; };
 
   // S^T of tile j (stage stage_idx) into s.
   auto qk = [&](int stage_idx, f32x16_t* s) {
@@ -356,11 +420,12 @@ __global__ __launch_bounds__(64 * W, OCC) void fwd_ring_kernel(const FwdArgs a, 
     wait_dma<2 * NPW, ST - 2>(min(ST - 2, n_tiles - 1 - j));
     __syncthreads();
     if (j + ST - 1 < n_tiles) issue(j + ST - 1, (stage_idx + ST - 1) % ST);
-    if (j >= wtiles) return;  // uniform per wave; the barrier is above
+    const int kt = j * SPAN + ks * BN;  // this wave's first key
+    if (kt >= wkend) return;  // uniform per wave; the barrier is above
 
     f32x16_t s[KB];
     qk(stage_idx, s);
-    if (masked(j)) mask(j * BN, s);
+    if (masked(kt)) mask(kt, s);
     const float mt = rowmax(s);
     // Rescale only when some row's max grew past the slack (always on the
     // first tile, where m_run is -inf).
@@ -383,14 +448,52 @@ __global__ __launch_bounds__(64 * W, OCC) void fwd_ring_kernel(const FwdArgs a, 
     for (int st = 0; st < ST; ++st)
       if (j0 + st < n_tiles) tile(j0 + st, st);
   }
-  __syncthreads();  // the ring is free for the output staging
+  __syncthreads();  // the ring is free for the merge and the output staging
+
+  // Merge the key splits of each row block through LDS; afterwards wave
+  // (rb, 0) stages its rows in the first merge slot of its row block (which
+  // only it reads) or, without splits, in its own region.
+  constexpr int ORS = S::kOutRow;
+  bf16_raw* stage;
+  if constexpr (KS > 1) {
+    constexpr int kPer = S::kMergeFloats;
+    float* const mf = reinterpret_cast<float*>(lds);
+    if (ks > 0) {
+      float* dst = mf + (rb * (KS - 1) + ks - 1) * kPer + lane;
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) dst[(db * 16 + r) * 64] = oacc[db][r];
+      dst[(DB * 16) * 64] = m_run;
+      dst[(DB * 16 + 1) * 64] = l_run;
+    }
+    __syncthreads();
+    if (ks > 0) return;  // no barrier follows
+#pragma unroll
+    for (int s2 = 1; s2 < KS; ++s2) {
+      const float* src = mf + (rb * (KS - 1) + s2 - 1) * kPer + lane;
+      const float m2 = src[(DB * 16) * 64];
+      const float l2 = src[(DB * 16 + 1) * 64];
+      const float mn = fmaxf(m_run, m2);
+      const float mu = mn == kNegInf ? 0.f : mn;
+      const float w1 = fast_exp2(m_run - mu);
+      const float w2 = fast_exp2(m2 - mu);
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) oacc[db][r] = oacc[db][r] * w1 + src[(db * 16 + r) * 64] * w2;
+      l_run = l_run * w1 + l2 * w2;
+      m_run = mn;
+    }
+    stage = reinterpret_cast<bf16_raw*>(mf + rb * (KS - 1) * kPer);
+  } else {
+    stage = reinterpret_cast<bf16_raw*>(lds) + rb * 32 * ORS;
+  }
   if (wrow0 >= sv.len_q) return;  // uniform per wave; no barrier follows
 
   // The half waves hold disjoint keys of the same rows.
   const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-  constexpr int ORS = S::kOutRow;
-  bf16_raw* const stage = reinterpret_cast<bf16_raw*>(lds) + wave * 32 * ORS;
   // Accumulator r of block db is column 32 db + 8 (r / 4) + 4 half + r % 4
   // of row r32: write the normalized rows to LDS ...
 #pragma unroll
@@ -421,28 +524,26 @@ __global__ __launch_bounds__(64 * W, OCC) void fwd_ring_kernel(const FwdArgs a, 
   }
 }
 
-template <int HD, int W, int BN, int ST, int OCC>
+template <int HD, int RB, int KS, int BN, int ST, int OCC>
 hipError_t launch_typed(const FwdArgs& a, hipStream_t stream) {
-  using S = RingShape<HD, W, BN, ST>;
+  using S = RingShape<HD, RB, KS, BN, ST>;
   const asrattn_fwd_params& p = a.p;
   const int q_tiles = (p.max_len_q + S::kBM - 1) / S::kBM;
   const long long total = (long long)q_tiles * p.heads_q * p.batch;
   if (total <= 0) return hipSuccess;
   if (total > 0x7fffffffLL) return hipErrorInvalidConfiguration;
-  hipLaunchKernelGGL((fwd_ring_kernel<HD, W, BN, ST, OCC>), dim3((unsigned)total), dim3(S::kThreads), 0, stream, a,
+  hipLaunchKernelGGL((fwd_ring_kernel<HD, RB, KS, BN, ST, OCC>), dim3((unsigned)total), dim3(S::kThreads), 0, stream, a,
                      q_tiles, (int)total);
   return hipGetLastError();
 }
 
 template <int HD>
 hipError_t launch_hd(const FwdArgs& a, hipStream_t stream) {
-  // 64-key tiles.  Head dim 128 on sequences longer than 128 rows: eight
-  // waves (256 query rows) share each tile through three stages, one
-  // workgroup per CU.  Otherwise four waves (128 rows), two stages, two or
-  // more workgroups per CU whose waves pair up on the SIMDs without sharing a
-  // barrier.
-  if (HD == 128 && a.p.max_len_q > 128) return launch_typed<HD, 8, 64, 3, 2>(a, stream);
-  return launch_typed<HD, 4, 64, 2, 2>(a, stream);
+  // Four waves (128 query rows) share each 64-key tile through two stages:
+  // two workgroups per CU, whose waves pair up on the SIMDs without sharing
+  // a barrier.  Key splits (KS > 1) halve the rows a CU holds at two waves
+  // per SIMD, which costs more than they save once the batch fills the GPU.
+  return launch_typed<HD, 4, 1, 64, 2, 2>(a, stream);
 }
 
 }  // namespace

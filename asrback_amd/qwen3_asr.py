@@ -5,7 +5,9 @@ Drop-in for the attention side of the reference's ``models/qwen3_asr.py``:
 ``RMSNorm``/``rotate`` (``:316-330``), ``KVCache`` (``:333-347``),
 ``TextAttention`` (``:350-432``) and ``TextModel`` (``:463-524``), with the
 same names, parameter names and signatures, and the cache layout
-``(layers, batch, length, kv_heads, head_dim)``.
+``(layers, batch, length, kv_heads, head_dim)``; and the transcriber's
+decode loop around them (``DecodeState``, ``choose``, ``TextGreedyDecoder``:
+``:659-699``, ``:1017-1214``).
 
 * Packed prompts and audio windows attend through
   :func:`asrback_amd.attention.varlen_attn` in every dtype (the reference
@@ -24,15 +26,20 @@ from __future__ import annotations
 from dataclasses import dataclass
 from typing import Callable
 
+import numpy as np
 import torch
 import torch.nn.functional as F
 from torch import Tensor, nn
 
 from .attention import KeyPrefix, decode, varlen_attn
-from .transcription import to_device
+from .transcription import CapturedGraph, to_device
 
 # Positions per row of the KV cache (qwen3_asr.py:57-59).
 CACHE_LENGTH = 1024
+# Decoder steps between host checks for finished rows (qwen3_asr.py:56).
+EOS_CHECK_INTERVAL = 4
+# Default cap on generated tokens per window (qwen3_asr.py:63).
+MAX_NEW_TOKENS = 512
 
 
 @dataclass
@@ -239,3 +246,219 @@ class TextModel(nn.Module):
             keys, values = cache.keys[index], cache.values[index]
             x = layer(x, lambda attention, h: attention.step(h, keys, values, positions, mask, cos, sin))
         return self.norm(x)
+
+
+@dataclass
+class DecodeState:
+    """Per-row decoding state updated in place by every step
+    (``qwen3_asr.py:659-699``).  ``position`` is each row's position of its
+    latest token; a step writes the next token to ``generated`` at
+    ``position + 1``.  Finished rows, and free rows (marked finished), keep
+    their token and position."""
+
+    tokens: Tensor  # (batch,)
+    position: Tensor  # (batch,)
+    end: Tensor  # (batch,), the last position a row may write
+    finished: Tensor  # (batch,)
+    sum_logprobs: Tensor  # (batch,)
+    generated: Tensor  # (batch, CACHE_LENGTH)
+
+    @classmethod
+    def allocate(cls, batch_size: int, device: torch.device) -> DecodeState:
+        return cls(
+            torch.zeros(batch_size, dtype=torch.long, device=device),
+            torch.zeros(batch_size, dtype=torch.long, device=device),
+            torch.zeros(batch_size, dtype=torch.long, device=device),
+            torch.ones(batch_size, dtype=torch.bool, device=device),
+            torch.zeros(batch_size, device=device),
+            torch.zeros((batch_size, CACHE_LENGTH), dtype=torch.long, device=device),
+        )
+
+    def narrow(self, batch_size: int) -> DecodeState:
+        return DecodeState(*(t[:batch_size] for t in (
+            self.tokens, self.position, self.end, self.finished, self.sum_logprobs, self.generated
+        )))
+
+    def free(self, rows: Tensor) -> None:
+        """Mark ``rows`` free: finished, at position 0."""
+        self.finished[rows] = True
+        self.position[rows] = 0
+        self.tokens[rows] = 0
+
+
+def choose(logits: Tensor, temperatures: Tensor | None = None) -> tuple[Tensor, Tensor]:
+    """Next token per row -- greedy, or sampled where the row's temperature is
+    positive -- and its log-probability (``qwen3_asr.py:1200-1210``)."""
+    token = logits.argmax(dim=-1)
+    if temperatures is not None:
+        scaled = logits / temperatures.clamp(min=1e-6)[:, None]
+        sampled = torch.multinomial(F.softmax(scaled, dim=-1), 1).squeeze(1)
+        token = torch.where(temperatures > 0, sampled, token)
+    logprob = F.log_softmax(logits, dim=-1).gather(1, token[:, None]).squeeze(1)
+    return token, logprob
+
+
+class TextGreedyDecoder:
+    """Decoding of Qwen3-ASR windows in a pool of ``max_batch_size`` cache
+    rows, the step replayed from a HIP graph per batch bucket.
+
+    Restates the decode path of the reference's ``Qwen3ASRTranscriber``
+    without its request queue, audio encoder and tokenizer: :meth:`admit`
+    runs prompts packed back to back straight into free rows and picks their
+    first tokens (``_admit``, ``qwen3_asr.py:1017-1090``), :meth:`step` is
+    ``_step`` (``:1179-1198``), :meth:`advance` runs up to
+    ``EOS_CHECK_INTERVAL`` steps from the graphs (``_advance``,
+    ``:1101-1128``; graphs as ``_capture_graphs``, ``:930-948``) and
+    :meth:`finished_rows` returns and frees finished rows (``_finish``,
+    ``:1131-1155``).  Attention reads each row's own keys, so one KV bucket
+    (the whole 1024-position slab) serves every length, as with the
+    reference's varlen path.
+    """
+
+    def __init__(self, text: TextModel, lm_head: nn.Module, config: dict, max_batch_size: int,
+                 eos_ids: list[int], graphs: bool = True) -> None:
+        self.text = text
+        self.lm_head = lm_head
+        self.config = config
+        weight = text.embed_tokens.weight
+        self.device, self.dtype = weight.device, weight.dtype
+        self.max_batch_size = max_batch_size
+        self.cos, self.sin = rope_tables(config, CACHE_LENGTH, self.device, self.dtype)
+        self.buckets = sorted(
+            {min(2**p, max_batch_size) for p in range(max_batch_size.bit_length())} | {max_batch_size}
+        )
+        self.kv_buckets = [CACHE_LENGTH]
+        self.cache = KVCache.allocate(config, max_batch_size, CACHE_LENGTH, self.device, self.dtype)
+        self.state = DecodeState.allocate(max_batch_size, self.device)
+        self.eos_ids = torch.tensor(eos_ids, dtype=torch.long, device=self.device)
+        self.rows: dict[int, dict] = {}
+        self.graphs: dict[tuple[int, int], CapturedGraph] = {}
+        if graphs:
+            self._capture_graphs()
+
+    @torch.inference_mode()
+    def _capture_graphs(self) -> None:
+        """One greedy step per (batch bucket, KV bucket); warm-up steps advance
+        the rows, so they start inside the cache."""
+        pool = torch.cuda.graph_pool_handle()
+        for batch_size in self.buckets:
+            state = self.state.narrow(batch_size)
+            for length in self.kv_buckets:
+                cache = self.cache.narrow(batch_size, length)
+                state.finished.zero_()
+                state.position.zero_()
+                state.end.fill_(CACHE_LENGTH - 1)
+                self.graphs[batch_size, length] = CapturedGraph(
+                    lambda state=state, cache=cache: self.step(state, cache), pool
+                )
+        self.state.free(torch.arange(self.max_batch_size, device=self.device))
+
+    def logits(self, hidden: Tensor) -> Tensor:
+        return self.lm_head(hidden).float()
+
+    @torch.inference_mode()
+    def admit(self, prompts: list[list[int]], max_new_tokens: int | list[int] = MAX_NEW_TOKENS,
+              embeddings: Tensor | None = None, audio_id: int | None = None,
+              temperatures: Tensor | None = None) -> list[int]:
+        """Prompt pass for new windows, packed back to back into free cache
+        rows, and their first tokens; returns their slots.  ``embeddings``
+        (one row per ``audio_id`` token of the packed prompts, in order)
+        replace those tokens' embeddings, as the audio encoder's output does."""
+        count = len(prompts)
+        slots = [s for s in range(self.max_batch_size) if s not in self.rows][:count]
+        if len(slots) < count:
+            raise RuntimeError("no free rows")
+        if isinstance(max_new_tokens, int):
+            max_new_tokens = [max_new_tokens] * count
+        lengths = [len(prompt) for prompt in prompts]
+        if min(lengths) < 1 or max(lengths) >= CACHE_LENGTH:
+            raise ValueError(f"prompt lengths must lie in [1, {CACHE_LENGTH})")
+        ids = np.concatenate([np.asarray(prompt, dtype=np.int64) for prompt in prompts])
+        offsets = np.cumsum(lengths) - lengths
+        positions = np.arange(len(ids)) - np.repeat(offsets, lengths)
+        limits = [min(n, CACHE_LENGTH - length) for n, length in zip(max_new_tokens, lengths)]
+        ends = [length - 1 + limit for length, limit in zip(lengths, limits)]
+        audio = np.flatnonzero(ids == audio_id) if audio_id is not None else None
+        ids_d, rows, positions_d, slot_rows, start, end = (
+            to_device(data, self.device)
+            for data in (ids, np.repeat(slots, lengths), positions, slots, lengths, ends)
+        )
+        x = self.text.embed_tokens(ids_d)
+        if embeddings is not None:
+            x[to_device(audio, self.device)] = embeddings.to(x.dtype)
+        segments = Segments.from_lengths(lengths, self.device)
+        hidden = self.text.prefill(x, self.cache, rows, positions_d, segments,
+                                   self.cos[positions_d], self.sin[positions_d])
+        last = segments.starts[1:].long() - 1
+        token, logprob = choose(self.logits(hidden[last]), temperatures)
+        state = self.state
+        state.tokens[slot_rows] = token
+        state.position[slot_rows] = start
+        state.end[slot_rows] = end
+        state.finished[slot_rows] = torch.isin(token, self.eos_ids) | (start >= end)
+        state.sum_logprobs[slot_rows] = logprob
+        state.generated[slot_rows, start] = token
+        for slot, length, end_position in zip(slots, lengths, ends):
+            self.rows[slot] = {"prompt_length": length, "end": end_position, "bound": length}
+        return slots
+
+    def step(self, state: DecodeState, cache: KVCache, temperatures: Tensor | None = None) -> None:
+        """Decode ``state.tokens`` and select every row's next token
+        (``qwen3_asr.py:1179-1198``)."""
+        hidden = self.text.step(state.tokens, state.position, cache, self.cos, self.sin)
+        token, logprob = choose(self.logits(hidden), temperatures)
+        active = ~state.finished
+        position = state.position + active
+        token = torch.where(active, token, state.tokens)
+        state.sum_logprobs.add_(logprob.masked_fill(state.finished, 0.0))
+        state.generated.scatter_(1, position[:, None], token[:, None])
+        state.finished.logical_or_(torch.isin(token, self.eos_ids) | (position >= state.end))
+        state.position.copy_(position)
+        state.tokens.copy_(token)
+
+    @torch.inference_mode()
+    def advance(self, temperatures: Tensor | None = None) -> int:
+        """Up to ``EOS_CHECK_INTERVAL`` steps over the occupied rows, from the
+        graph of the smallest covering batch bucket when every row is greedy;
+        returns the count."""
+        bucket = next(size for size in self.buckets if size > max(self.rows))
+        rows = self.rows.values()
+        count = max(1, min(EOS_CHECK_INTERVAL, max(r["end"] - r["bound"] for r in rows)))
+        length = max(min(r["bound"] + count, r["end"]) for r in rows) + 1
+        kv_bucket = next(size for size in self.kv_buckets if size >= length)
+        if self.graphs and temperatures is None:
+            graph = self.graphs[bucket, kv_bucket]
+            for _ in range(count):
+                graph.replay()
+        else:
+            state = self.state.narrow(bucket)
+            cache = self.cache.narrow(bucket, kv_bucket)
+            for _ in range(count):
+                self.step(state, cache, temperatures)
+        for r in rows:
+            r["bound"] = min(r["bound"] + count, r["end"])
+        return count
+
+    @torch.inference_mode()
+    def finished_rows(self) -> dict[int, tuple[list[int], float]]:
+        """Generated tokens and mean log-probability of the rows that finished,
+        which are freed (``qwen3_asr.py:1131-1155``; a trailing EOS is
+        dropped)."""
+        finished = self.state.finished[: max(self.rows) + 1].tolist()
+        done = [slot for slot in self.rows if finished[slot]]
+        if not done:
+            return {}
+        rows = torch.tensor(done, device=self.device)
+        positions = self.state.position[rows].tolist()
+        sums = self.state.sum_logprobs[rows].tolist()
+        generated = self.state.generated[rows, : max(positions) + 1].tolist()
+        self.state.free(rows)
+        eos = set(self.eos_ids.tolist())
+        out = {}
+        for slot, position, total, tokens in zip(done, positions, sums, generated):
+            row = self.rows.pop(slot)
+            tokens = tokens[row["prompt_length"] : position + 1]
+            if tokens and tokens[-1] in eos:
+                tokens.pop()
+            out[slot] = (tokens, total / (len(tokens) + 1))
+        return out

@@ -117,3 +117,42 @@ class AudioAttention(nn.Module):
     def forward(self, x: Tensor, segments: oa.Segments) -> Tensor:
         q, k, v = (p(x).view(len(x), self.heads, -1) for p in (self.q_proj, self.k_proj, self.v_proj))
         return self.out_proj(oa.qwen_attend(q, k, v, segments, causal=False).flatten(1))
+
+
+def greedy_decode(model: TextModel, lm_head: Tensor, config: dict, prompt: list[int], max_new_tokens: int,
+                  eos_ids: list[int], cache_length: int = 1024) -> dict:
+    """The Qwen3-ASR transcriber's token loop for one window, greedy
+    (``qwen3_asr.py:1017-1090``, ``:1179-1198``, ``:1131-1155``): the prompt
+    pass picks the first token at position ``len(prompt)``; each step decodes
+    the latest token at its position and picks the next; a window stops at an
+    EOS id or when its position reaches ``len(prompt) - 1 + limit``, with
+    ``limit = min(max_new_tokens, cache_length - len(prompt))``; a trailing EOS
+    is dropped.  Returns the tokens and the smallest top-2 logit gap met (how
+    far the argmaxes are from ties)."""
+    n = len(prompt)
+    end = n - 1 + min(max_new_tokens, cache_length - n)
+    shape = (config["num_hidden_layers"], 1, cache_length, config["num_key_value_heads"], config["head_dim"])
+    keys, values = torch.zeros(shape), torch.zeros(shape)
+    cos, sin = oa.rope_tables(config["rope_theta"], config["head_dim"], cache_length, torch.float32)
+    positions = torch.arange(n)
+    gaps = []
+
+    def pick(hidden: Tensor) -> int:
+        logits = hidden @ lm_head.T
+        top = torch.topk(logits, 2).values
+        gaps.append(float(top[0] - top[1]))
+        return int(logits.argmax())
+
+    with torch.inference_mode():
+        x = model.embed_tokens(torch.tensor(prompt))
+        hidden = model.prefill(x, keys, values, torch.zeros(n, dtype=torch.long), positions,
+                               oa.Segments.from_lengths([n]), cos[positions], sin[positions])
+        token, position = pick(hidden[-1]), n
+        tokens = [token]
+        while token not in eos_ids and position < end:
+            hidden = model.step(torch.tensor([token]), torch.tensor([position]), keys, values, cos, sin)
+            token, position = pick(hidden[0]), position + 1
+            tokens.append(token)
+    if tokens[-1] in eos_ids:
+        tokens.pop()
+    return {"tokens": tokens, "min_gap": min(gaps)}

@@ -230,3 +230,62 @@ def test_qwen_audio_attention_windows(device):
         expected = ref(x, oa.Segments.from_lengths(lengths))
         out = model(x.to(device), aq.Segments.from_lengths(lengths, device))
     assert max_rel_err(out.cpu(), expected) < 1e-4
+
+
+def _qwen_decoder(device, graphs, eos_ids):
+    from asrback_amd import qwen3_asr as aq
+
+    ref, model = qwen_pair(device)
+    g = torch.Generator().manual_seed(21)
+    head = torch.randn(QWEN3["vocab_size"], QWEN3["hidden_size"], generator=g) * 16 * QWEN3["hidden_size"] ** -0.5
+    prompts = [torch.randint(0, QWEN3["vocab_size"], (n,), generator=g).tolist() for n in (37, 52, 29)]
+    lm_head = torch.nn.Linear(QWEN3["hidden_size"], QWEN3["vocab_size"], bias=False)
+    lm_head.weight.data.copy_(head)
+    decoder = aq.TextGreedyDecoder(model, lm_head.to(device), QWEN3, 4, eos_ids, graphs=graphs)
+    expected = [oq.greedy_decode(ref, head, QWEN3, p, 12, eos_ids) for p in prompts]
+    for e in expected:
+        assert e["min_gap"] > 0.1  # far from argmax ties
+    return decoder, prompts, [e["tokens"] for e in expected]
+
+
+def _drain(decoder, results):
+    while decoder.rows:
+        decoder.advance()
+        for slot, (tokens, _) in decoder.finished_rows().items():
+            results[slot] = tokens
+
+
+def test_qwen_greedy_decoder_matches_oracle(device):
+    """Qwen3 transcriber loop on the kernels -- packed prompts prefilled into
+    free rows, graph-replayed steps, EOS checks every few steps -- emits the
+    oracle's greedy tokens; EOS id 989 ends the third window early."""
+    say("qwen3 greedy decoder, graphs")
+    decoder, prompts, expected = _qwen_decoder(device, True, [989])
+    assert 989 not in expected[2] and len(expected[2]) < 12 and len(expected[0]) == 12
+    slots = decoder.admit(prompts, 12)
+    results = {}
+    _drain(decoder, results)
+    assert [results[s] for s in slots] == expected
+
+
+def test_qwen_greedy_decoder_staggered_rows(device):
+    """Windows admitted while others are mid-decode get the same tokens as
+    alone: rows do not interact."""
+    say("qwen3 greedy decoder, staggered admission")
+    decoder, prompts, expected = _qwen_decoder(device, True, [])
+    first = decoder.admit(prompts[:2], 12)
+    results = {}
+    decoder.advance()
+    third = decoder.admit(prompts[2:], 12)
+    _drain(decoder, results)
+    assert [results[s] for s in first + third] == expected
+
+
+def test_qwen_greedy_decoder_eager_equals_graphs(device):
+    """Eager steps give the graphs' tokens."""
+    say("qwen3 greedy decoder, eager")
+    decoder, prompts, expected = _qwen_decoder(device, False, [])
+    slots = decoder.admit(prompts, 12)
+    results = {}
+    _drain(decoder, results)
+    assert [results[s] for s in slots] == expected
