@@ -19,7 +19,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must be imported before the library; see above)
 
 LIBRARY = Path(__file__).resolve().with_name("libasrattn.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 # enum asrattn_status / asrattn_dtype / asrattn_causal
 OK = 0
@@ -106,12 +106,35 @@ class DecodeParams(ctypes.Structure):
     ]
 
 
+class AppendParams(ctypes.Structure):
+    """``asrattn_append_params``."""
+
+    _fields_ = [
+        ("k_new", _ptr),
+        ("v_new", _ptr),
+        ("kn_batch_stride", _i64),
+        ("kn_head_stride", _i64),
+        ("vn_batch_stride", _i64),
+        ("vn_head_stride", _i64),
+        ("q_norm", _ptr),
+        ("k_norm", _ptr),
+        ("eps", ctypes.c_float),
+        ("cos", _ptr),
+        ("sin", _ptr),
+        ("rope_batch_stride", _i64),
+    ]
+
+
 # Every symbol include/asrattn.h declares, with (restype, argtypes).
 SIGNATURES = {
     "asrattn_fwd": (ctypes.c_int, [ctypes.POINTER(FwdParams), _ptr]),
     "asrattn_decode": (
         ctypes.c_int,
         [ctypes.POINTER(DecodeParams), _ptr, ctypes.c_size_t, _ptr],
+    ),
+    "asrattn_decode_append": (
+        ctypes.c_int,
+        [ctypes.POINTER(DecodeParams), ctypes.POINTER(AppendParams), _ptr, ctypes.c_size_t, _ptr],
     ),
     "asrattn_decode_workspace_size": (ctypes.c_size_t, [ctypes.POINTER(DecodeParams)]),
     "asrattn_decode_num_splits": (ctypes.c_int, [ctypes.POINTER(DecodeParams)]),

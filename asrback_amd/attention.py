@@ -313,6 +313,95 @@ def decode(
     return out
 
 
+def decode_append(
+    q: Tensor,
+    k_new: Tensor,
+    v_new: Tensor,
+    k: Tensor,
+    v: Tensor,
+    positions: Tensor,
+    *,
+    q_norm: Tensor | None = None,
+    k_norm: Tensor | None = None,
+    eps: float = 1e-6,
+    cos: Tensor | None = None,
+    sin: Tensor | None = None,
+    num_splits: int = 0,
+    scale: float | None = None,
+    out: Tensor | None = None,
+    workspace: Tensor | None = None,
+) -> Tensor:
+    """A decoder step with its prologue fused in (``asrattn_decode_append``):
+    q ``(batch, heads_q, head_dim)`` and the step's key ``k_new`` ``(batch,
+    heads_kv, head_dim)`` get the per-head RMSNorm (``q_norm``/``k_norm``
+    weights ``(head_dim,)``, or neither) and the rotary embedding (``cos``/
+    ``sin`` ``(batch, head_dim)`` at each row's position, or neither); the
+    new key and ``v_new`` are written to the cache ``k``/``v`` ``(batch,
+    length, heads_kv, head_dim)`` at ``positions`` (int64), and the query
+    attends keys ``0 .. positions[b]``.  Replaces the step path of
+    ``TextAttention._project`` and ``step`` (``qwen3_asr.py:366-372``,
+    ``:409-432``) and Whisper's cache scatter (``whisper.py:224-228``).
+    Returns ``(batch, heads_q, head_dim)``."""
+    if q.dim() != 3 or k.dim() != 4 or v.shape != k.shape:
+        raise ValueError(
+            f"decode_append expects q (B, Hq, D) and k/v (B, L, Hkv, D); got {tuple(q.shape)}, "
+            f"{tuple(k.shape)}, {tuple(v.shape)}"
+        )
+    batch, heads_kv, head_dim = k.shape[0], k.shape[2], k.shape[3]
+    if q.shape[0] != batch or q.shape[2] != head_dim or q.shape[1] % heads_kv:
+        raise ValueError("q and k disagree on batch, head_dim or head grouping")
+    for name, t in (("k_new", k_new), ("v_new", v_new)):
+        if t.shape != (batch, heads_kv, head_dim):
+            raise ValueError(f"{name} must be ({batch}, {heads_kv}, {head_dim}), got {tuple(t.shape)}")
+    if (q_norm is None) != (k_norm is None) or (cos is None) != (sin is None):
+        raise ValueError("q_norm/k_norm and cos/sin come in pairs")
+    if positions.dtype != torch.int64 or positions.shape != (batch,):
+        raise ValueError(f"positions must be int64 ({batch},)")
+    _dtype_code(q, k, v, k_new, v_new)
+    extras = [t for t in (q_norm, k_norm, cos, sin) if t is not None]
+    for t in extras:
+        if t.dtype != q.dtype:
+            raise TypeError("norm weights and rotary tables must have the cache's dtype")
+    if q_norm is not None and (q_norm.shape != (head_dim,) or k_norm.shape != (head_dim,)):
+        raise ValueError(f"norm weights must be ({head_dim},)")
+    if cos is not None and (cos.shape != (batch, head_dim) or sin.shape != (batch, head_dim)):
+        raise ValueError(f"cos/sin must be ({batch}, {head_dim})")
+    q = _aligned(q, (0, 1))
+    k_new, v_new = (_aligned(t, (0, 1)) for t in (k_new, v_new))
+    if q_norm is not None:
+        q_norm, k_norm = q_norm.contiguous(), k_norm.contiguous()
+    if cos is not None:
+        cos, sin = cos.contiguous(), sin.contiguous()
+    if k.stride(-1) != 1 or v.stride(-1) != 1:
+        raise ValueError("the cache needs a unit last stride (it is written in place)")
+    if out is None:
+        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    elif out.shape != q.shape or out.dtype != q.dtype or out.stride(-1) != 1:
+        raise ValueError("out must match q's shape and dtype, with a unit last stride")
+    positions = positions.contiguous()
+    device = _check_device(q, k, v, out, positions, k_new, v_new, *extras)
+    params = _decode_params(q, k, v, out, None, positions, num_splits, scale)
+    app = _lib.AppendParams()
+    app.k_new, app.v_new = k_new.data_ptr(), v_new.data_ptr()
+    app.kn_batch_stride, app.kn_head_stride = k_new.stride(0), k_new.stride(1)
+    app.vn_batch_stride, app.vn_head_stride = v_new.stride(0), v_new.stride(1)
+    app.q_norm = _ptr(q_norm)
+    app.k_norm = _ptr(k_norm)
+    app.eps = eps
+    app.cos, app.sin = _ptr(cos), _ptr(sin)
+    app.rope_batch_stride = 0 if cos is None else cos.stride(0)
+    lib = _lib.load()
+    need = lib.asrattn_decode_workspace_size(ctypes.byref(params))
+    if workspace is None and need and need != ctypes.c_size_t(-1).value:
+        workspace = decode_workspace(need, device)
+    size = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    _lib.check(
+        lib.asrattn_decode_append(ctypes.byref(params), ctypes.byref(app), _ptr(workspace), size, _stream(device)),
+        "asrattn_decode_append",
+    )
+    return out
+
+
 # Decode workspaces per device: one buffer serves every call on the device
 # (calls on one device run in stream order); grown buffers are kept alive
 # because graphs captured earlier still hold their addresses.

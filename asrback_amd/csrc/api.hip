@@ -157,7 +157,10 @@ int asrattn_decode_num_splits(const asrattn_decode_params* params) {
 
 
 
-int asrattn_decode(const asrattn_decode_params* params, void* workspace, size_t workspace_bytes, void* stream) {
+namespace {
+
+int run_decode(const asrattn_decode_params* params, const asrattn_append_params* append, void* workspace,
+               size_t workspace_bytes, void* stream, const char* name) {
   int rc = check_decode(params);
   if (rc != ASRATTN_OK) return rc;
   const asrattn_decode_params& p = *params;
@@ -169,6 +172,23 @@ int asrattn_decode(const asrattn_decode_params* params, void* workspace, size_t 
       !vec_aligned(p.v, p.dtype, {p.v_batch_stride, p.v_token_stride, p.v_head_stride}))
     return fail(ASRATTN_ERR_INVALID,
                 "q, k and v need 16-byte aligned pointers and strides that are multiples of 16 bytes");
+  if (append != nullptr) {
+    const asrattn_append_params& ap = *append;
+    if (p.positions == nullptr || p.seqused_k != nullptr)
+      return fail(ASRATTN_ERR_INVALID, "the appending step takes positions and no seqused_k");
+    if (ap.k_new == nullptr || ap.v_new == nullptr)
+      return fail(ASRATTN_ERR_INVALID, "k_new and v_new must be non-NULL");
+    if ((ap.q_norm == nullptr) != (ap.k_norm == nullptr) || (ap.cos == nullptr) != (ap.sin == nullptr))
+      return fail(ASRATTN_ERR_INVALID, "q_norm/k_norm and cos/sin come in pairs");
+    if (!(ap.eps >= 0.f && ap.eps < 1e30f)) return fail(ASRATTN_ERR_INVALID, "eps must be finite and >= 0");
+    if (!vec_aligned(ap.k_new, p.dtype, {ap.kn_batch_stride, ap.kn_head_stride}) ||
+        !vec_aligned(ap.v_new, p.dtype, {ap.vn_batch_stride, ap.vn_head_stride}) ||
+        (ap.q_norm != nullptr && (!vec_aligned(ap.q_norm, p.dtype, {}) || !vec_aligned(ap.k_norm, p.dtype, {}))) ||
+        (ap.cos != nullptr &&
+         (!vec_aligned(ap.cos, p.dtype, {ap.rope_batch_stride}) || !vec_aligned(ap.sin, p.dtype, {ap.rope_batch_stride}))))
+      return fail(ASRATTN_ERR_INVALID,
+                  "k_new, v_new, the norm weights and cos/sin need 16-byte aligned pointers and strides");
+  }
   // Keys are addressed with 32-bit byte offsets from the sequence's start.
   const long long es = p.dtype == ASRATTN_BF16 ? 2 : 4;
   if ((long long)p.max_len_k * p.k_token_stride * es >= (1LL << 31) ||
@@ -188,8 +208,19 @@ int asrattn_decode(const asrattn_decode_params* params, void* workspace, size_t 
     ws_o = reinterpret_cast<float*>(base + w.partials);
     ws_ml = reinterpret_cast<float*>(base + w.stats);
   }
-  return from_hip(asrattn::launch_decode(p, s, ws_o, ws_ml, static_cast<hipStream_t>(stream)),
-                  "asrattn_decode");
+  return from_hip(asrattn::launch_decode(p, append, s, ws_o, ws_ml, static_cast<hipStream_t>(stream)), name);
+}
+
+}  // namespace
+
+int asrattn_decode(const asrattn_decode_params* params, void* workspace, size_t workspace_bytes, void* stream) {
+  return run_decode(params, nullptr, workspace, workspace_bytes, stream, "asrattn_decode");
+}
+
+int asrattn_decode_append(const asrattn_decode_params* params, const asrattn_append_params* append,
+                          void* workspace, size_t workspace_bytes, void* stream) {
+  if (append == nullptr) return fail(ASRATTN_ERR_INVALID, "append parameters must be non-NULL");
+  return run_decode(params, append, workspace, workspace_bytes, stream, "asrattn_decode_append");
 }
 
 }  // extern "C"

@@ -33,6 +33,7 @@ namespace {
 
 struct DecodeArgs {
   asrattn_decode_params p;
+  asrattn_append_params ap;  // the fused prologue (append variant only)
   float* ws_o;   // [batch][heads_q][splits][head_dim]
   float* ws_ml;  // [batch][heads_q][splits][2]
   int splits;
@@ -96,6 +97,67 @@ __device__ __forceinline__ void unpack<bf16_raw>(const uint4& r, float* out) {
   out[6] = bf16_lo(r.w); out[7] = bf16_hi(r.w);
 }
 
+template <typename T>
+__device__ __forceinline__ uint4 pack(const float* x);
+
+template <>
+__device__ __forceinline__ uint4 pack<float>(const float* x) {
+  return make_uint4(__float_as_uint(x[0]), __float_as_uint(x[1]), __float_as_uint(x[2]), __float_as_uint(x[3]));
+}
+
+template <>
+__device__ __forceinline__ uint4 pack<bf16_raw>(const float* x) {
+  return make_uint4(pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3]), pack_bf16x2(x[4], x[5]), pack_bf16x2(x[6], x[7]));
+}
+
+// x rounded to T (and back): where the reference's element-wise ops round.
+template <typename T>
+__device__ __forceinline__ float round_to(float x) {
+  if constexpr (sizeof(T) == 2) return bf16_to_f32(f32_to_bf16(x));
+  return x;
+}
+
+// Per-head RMSNorm and rotary embedding of one row slice -- lane `sub` of
+// the LPK lanes holding a head_dim row, EPL elements -- in the reference's
+// rounding order (qwen3_asr.py:322-330): the norm x * rsqrt(mean(x^2) +
+// eps) * w in fp32, rounded once; the rotation x c + r s with r = (-x[d/2:],
+// x[:d/2]) rounded after each product and after the sum.  Element e of lane
+// sub pairs with element e of lane sub ^ LPK/2.  w, cs and sn are the
+// lane's slices of the weights and tables (loaded by the caller); has_norm
+// and has_rot are uniform over the grid.  All lanes of the wave must take
+// part.
+template <typename T, int HD, int LPK>
+__device__ __forceinline__ uint4 norm_rotate(uint4 raw, bool has_norm, const uint4& w, bool has_rot, const uint4& cs,
+                                             const uint4& sn, float eps, int sub) {
+  constexpr int EPL = Elem<T>::kPerVec;
+  float x[EPL];
+  unpack<T>(raw, x);
+  if (has_norm) {
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) ss = fmaf(x[e], x[e], ss);
+    ss = group_sum<LPK>(ss);
+    const float r = rsqrtf(ss * (1.f / HD) + eps);
+    float wv[EPL];
+    unpack<T>(w, wv);
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) x[e] = round_to<T>(x[e] * r * wv[e]);
+  }
+  if (has_rot) {
+    float cv[EPL], sv[EPL];
+    unpack<T>(cs, cv);
+    unpack<T>(sn, sv);
+    const bool lower = sub < LPK / 2;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      const float partner = __shfl_xor(x[e], LPK / 2, 64);
+      const float rot = lower ? -partner : partner;
+      x[e] = round_to<T>(round_to<T>(x[e] * cv[e]) + round_to<T>(rot * sv[e]));
+    }
+  }
+  return pack<T>(x);
+}
+
 // Online-softmax state of one stream for the G query heads of a kv head.
 template <typename T, int HD, int G, int W>
 struct Stream {
@@ -104,6 +166,23 @@ struct Stream {
   uint4 q[G];   // the lane's raw 16-byte slice of each query head
   float c;      // scale * log2(e), applied to the reduced score
   float m[G], l[G], o[G][EPL];
+
+  // Starts the state from one key (k, v) when `mine`; the dot products run
+  // on every lane (their reductions need the whole wave).
+  __device__ __forceinline__ void seed(const uint4& k, const uint4& v, bool mine) {
+    float vf[EPL];
+    unpack<T>(v, vf);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float s = group_sum<S::kLPK>(dot16<T>(q[g], k)) * c;
+      if (mine) {
+        m[g] = s;
+        l[g] = 1.f;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) o[g][e] = vf[e];
+      }
+    }
+  }
 
   __device__ __forceinline__ void init() {
 #pragma unroll
@@ -180,7 +259,14 @@ struct Stream {
 
 // At most 128 VGPRs, so that four waves fit per SIMD (two 8-wave workgroups
 // per CU).
-template <typename T, int HD, int G, int W>
+//
+// APPEND: the fused prologue of asrattn_decode_append.  q and the step's key
+// are normalized and rotated in registers; the cache supplies keys
+// 0 .. positions[b] - 1 and the new key/value join from registers (the last
+// split folds them into its state); the first split writes them to the
+// cache at positions[b].  No workgroup reads that slot, so splits need no
+// ordering among themselves.
+template <typename T, int HD, int G, int W, bool APPEND>
 __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeArgs a) {
   using S = DecodeShape<T, HD, G, W>;
   constexpr int EPL = S::kEPL, LPK = S::kLPK, NS = S::kStreams, U = S::kUnroll, STEP = S::kStep;
@@ -194,7 +280,9 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeArgs a) {
   const int sub = lane % LPK;
   const int stream = wave * S::kKPW + lane / LPK;
 
-  const int n = decode_key_count(p.seqused_k, p.positions, b, p.max_len_k);
+  const int64_t pos = APPEND ? p.positions[b] : 0;
+  const int n = APPEND ? (int)min(max(pos, (int64_t)0), (int64_t)p.max_len_k)
+                       : decode_key_count(p.seqused_k, p.positions, b, p.max_len_k);
   const int chunk = (n + a.splits - 1) / a.splits;
   const int k0 = min(n, split * chunk);
   const int k1 = min(n, k0 + chunk);
@@ -210,6 +298,29 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeArgs a) {
   }
   st.c = a.c;
   st.init();
+  // The prologue's inputs load here, before the first K/V batch; its
+  // arithmetic runs after that batch is issued.
+  const asrattn_append_params& ap = a.ap;
+  const bool has_norm = APPEND && ap.q_norm != nullptr;
+  const bool has_rot = APPEND && ap.cos != nullptr;
+  uint4 knew = {}, vnew = {}, qw = {}, kw = {}, cs = {}, sn = {};
+  if constexpr (APPEND) {
+    const T* knp = static_cast<const T*>(ap.k_new) + (int64_t)b * ap.kn_batch_stride + (int64_t)hkv * ap.kn_head_stride;
+    const T* vnp = static_cast<const T*>(ap.v_new) + (int64_t)b * ap.vn_batch_stride + (int64_t)hkv * ap.vn_head_stride;
+    // Absent weights or tables read k_new's slice instead (and are unused):
+    // the loads stay unconditional, so no branch joins their registers and
+    // forces a wait before the first K/V batch.
+    const T* qwp = has_norm ? static_cast<const T*>(ap.q_norm) : knp;
+    const T* kwp = has_norm ? static_cast<const T*>(ap.k_norm) : knp;
+    const T* csp = has_rot ? static_cast<const T*>(ap.cos) + (int64_t)b * ap.rope_batch_stride : knp;
+    const T* snp = has_rot ? static_cast<const T*>(ap.sin) + (int64_t)b * ap.rope_batch_stride : knp;
+    knew = *reinterpret_cast<const uint4*>(knp + sub * EPL);
+    vnew = *reinterpret_cast<const uint4*>(vnp + sub * EPL);
+    qw = *reinterpret_cast<const uint4*>(qwp + sub * EPL);
+    kw = *reinterpret_cast<const uint4*>(kwp + sub * EPL);
+    cs = *reinterpret_cast<const uint4*>(csp + sub * EPL);
+    sn = *reinterpret_cast<const uint4*>(snp + sub * EPL);
+  }
 
   // K and V of this (sequence, kv head) through buffer resources that end
   // at the split's last key: loads past it return zeros without a branch,
@@ -244,12 +355,26 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeArgs a) {
   uint4 ka[U], va[U], kb[U], vb[U];
   unsigned mb = 0;
   unsigned ma = load(ka, va, k0);
+  if constexpr (APPEND) {
+    __builtin_amdgcn_sched_barrier(0);  // keep the prologue below the batch's issue
+#pragma unroll
+    for (int g = 0; g < G; ++g) st.q[g] = norm_rotate<T, HD, LPK>(st.q[g], has_norm, qw, has_rot, cs, sn, ap.eps, sub);
+    knew = norm_rotate<T, HD, LPK>(knew, has_norm, kw, has_rot, cs, sn, ap.eps, sub);
+    st.seed(knew, vnew, split == a.splits - 1 && stream == 0);
+  }
   for (int base = k0; base < k1; base += 2 * STEP) {
     mb = load(kb, vb, base + STEP);
     st.consume(ka, va, ma);
     if (base + STEP >= k1) break;
     ma = load(ka, va, base + 2 * STEP);
     st.consume(kb, vb, mb);
+  }
+
+  if constexpr (APPEND) {
+    if (split == 0 && stream == 0 && pos >= 0 && pos < p.max_len_k) {
+      *reinterpret_cast<uint4*>(const_cast<char*>(kbase) + (int64_t)pos * kts + lane_bytes) = knew;
+      *reinterpret_cast<uint4*>(const_cast<char*>(vbase) + (int64_t)pos * vts + lane_bytes) = vnew;
+    }
   }
 
   st.merge_wave();
@@ -322,10 +447,13 @@ __global__ __launch_bounds__(HD) void decode_combine_kernel(const DecodeArgs a) 
 }
 
 template <typename T, int HD, int G, int W>
-hipError_t launch_typed(const DecodeArgs& a, hipStream_t stream) {
+hipError_t launch_typed(const DecodeArgs& a, bool append, hipStream_t stream) {
   const asrattn_decode_params& p = a.p;
   dim3 grid(a.splits, p.heads_kv, p.batch);
-  hipLaunchKernelGGL((decode_kernel<T, HD, G, W>), grid, dim3(64 * W), 0, stream, a);
+  if (append)
+    hipLaunchKernelGGL((decode_kernel<T, HD, G, W, true>), grid, dim3(64 * W), 0, stream, a);
+  else
+    hipLaunchKernelGGL((decode_kernel<T, HD, G, W, false>), grid, dim3(64 * W), 0, stream, a);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || a.splits == 1) return err;
   hipLaunchKernelGGL((decode_combine_kernel<T, HD>), dim3(p.heads_q, p.batch), dim3(HD), 0, stream, a);
@@ -333,20 +461,20 @@ hipError_t launch_typed(const DecodeArgs& a, hipStream_t stream) {
 }
 
 template <typename T, int HD, int G>
-hipError_t launch_waves(const DecodeArgs& a, int waves, hipStream_t stream) {
+hipError_t launch_waves(const DecodeArgs& a, int waves, bool append, hipStream_t stream) {
   switch (waves) {
-    case 4: return launch_typed<T, HD, G, 4>(a, stream);
-    case 8: return launch_typed<T, HD, G, 8>(a, stream);
-    default: return launch_typed<T, HD, G, 16>(a, stream);
+    case 4: return launch_typed<T, HD, G, 4>(a, append, stream);
+    case 8: return launch_typed<T, HD, G, 8>(a, append, stream);
+    default: return launch_typed<T, HD, G, 16>(a, append, stream);
   }
 }
 
 template <typename T, int HD>
-hipError_t launch_hd(const DecodeArgs& a, int group, int waves, hipStream_t stream) {
+hipError_t launch_hd(const DecodeArgs& a, int group, int waves, bool append, hipStream_t stream) {
   switch (group) {
-    case 1: return launch_waves<T, HD, 1>(a, waves, stream);
-    case 2: return launch_waves<T, HD, 2>(a, waves, stream);
-    case 4: return launch_waves<T, HD, 4>(a, waves, stream);
+    case 1: return launch_waves<T, HD, 1>(a, waves, append, stream);
+    case 2: return launch_waves<T, HD, 2>(a, waves, append, stream);
+    case 4: return launch_waves<T, HD, 4>(a, waves, append, stream);
     default: return hipErrorInvalidValue;
   }
 }
@@ -372,10 +500,12 @@ int decode_waves(const asrattn_decode_params& p, int splits) {
   return waves;
 }
 
-hipError_t launch_decode(const asrattn_decode_params& p, int splits, float* ws_o, float* ws_ml,
-                         hipStream_t stream) {
+hipError_t launch_decode(const asrattn_decode_params& p, const asrattn_append_params* append, int splits,
+                         float* ws_o, float* ws_ml, hipStream_t stream) {
   DecodeArgs a;
   a.p = p;
+  a.ap = append != nullptr ? *append : asrattn_append_params{};
+  const bool app = append != nullptr;
   a.ws_o = ws_o;
   a.ws_ml = ws_ml;
   a.splits = splits;
@@ -383,11 +513,11 @@ hipError_t launch_decode(const asrattn_decode_params& p, int splits, float* ws_o
   const int group = p.heads_q / p.heads_kv;
   const int waves = decode_waves(p, splits);
   if (p.dtype == ASRATTN_BF16) {
-    return p.head_dim == 64 ? launch_hd<bf16_raw, 64>(a, group, waves, stream)
-                            : launch_hd<bf16_raw, 128>(a, group, waves, stream);
+    return p.head_dim == 64 ? launch_hd<bf16_raw, 64>(a, group, waves, app, stream)
+                            : launch_hd<bf16_raw, 128>(a, group, waves, app, stream);
   }
-  return p.head_dim == 64 ? launch_hd<float, 64>(a, group, waves, stream)
-                          : launch_hd<float, 128>(a, group, waves, stream);
+  return p.head_dim == 64 ? launch_hd<float, 64>(a, group, waves, app, stream)
+                          : launch_hd<float, 128>(a, group, waves, app, stream);
 }
 
 }  // namespace asrattn

@@ -12,8 +12,9 @@ namespace asrattn {
 // splits > 1 the workspace holds the partial outputs
 // float[batch][heads_q][splits][head_dim] and (max, sum) pairs
 // float[batch][heads_q][splits][2], merged by a second kernel.
-hipError_t launch_decode(const asrattn_decode_params& p, int splits, float* ws_o, float* ws_ml,
-                         hipStream_t stream);
+// append: the fused prologue of asrattn_decode_append, or null.
+hipError_t launch_decode(const asrattn_decode_params& p, const asrattn_append_params* append, int splits,
+                         float* ws_o, float* ws_ml, hipStream_t stream);
 int decode_waves(const asrattn_decode_params& p, int splits);
 bool decode_supported(int dtype, int head_dim, int group);
 

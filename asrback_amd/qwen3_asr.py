@@ -31,7 +31,7 @@ import torch
 import torch.nn.functional as F
 from torch import Tensor, nn
 
-from .attention import KeyPrefix, decode, varlen_attn
+from .attention import KeyPrefix, decode, decode_append, varlen_attn
 from .transcription import CapturedGraph, to_device
 
 # Positions per row of the KV cache (qwen3_asr.py:57-59).
@@ -180,10 +180,34 @@ class TextAttention(nn.Module):
         values[rows, positions] = v
         return self.o_proj(attend(q, k, v, segments, causal=True).flatten(1))
 
+    def _fused_step(self, x: Tensor, keys: Tensor) -> bool:
+        return (
+            x.dtype in (torch.float32, torch.bfloat16)
+            and self.head_dim in (64, 128)
+            and self.heads // self.kv_heads in (1, 2, 4)
+            and keys.dtype == x.dtype
+        )
+
     def step(self, x, keys, values, positions, mask, cos, sin) -> Tensor:
         """One token per row at its own position, attending over the cache
         view ``keys``/``values`` ``(batch, length, kv_heads, head_dim)``
-        (``:392-432``)."""
+        (``:392-432``).  With the step mask built on these positions (a
+        :class:`KeyPrefix` of ``positions``, as :meth:`TextModel.step`
+        passes), the norms, the rotation, the cache write and the attention
+        run as one kernel (:func:`~asrback_amd.attention.decode_append`);
+        other mask forms take the reference's sequence of ops."""
+        if isinstance(mask, KeyPrefix) and mask.positions is positions and self._fused_step(x, keys):
+            batch = len(x)
+            q, k, v = self.qkv_proj(x).split(self.sizes, dim=-1)
+            output = decode_append(
+                q.view(batch, self.heads, self.head_dim),
+                k.view(batch, self.kv_heads, self.head_dim),
+                v.view(batch, self.kv_heads, self.head_dim),
+                keys, values, positions,
+                q_norm=self.q_norm.weight, k_norm=self.k_norm.weight, eps=self.q_norm.eps,
+                cos=cos, sin=sin,
+            )
+            return self.o_proj(output.flatten(1))
         q, k, v = self._project(x, cos, sin)
         rows = torch.arange(len(x), device=x.device)
         keys[rows, positions] = k
@@ -241,7 +265,7 @@ class TextModel(nn.Module):
         del varlen
         x = self.embed_tokens(tokens)
         cos, sin = cos[positions], sin[positions]
-        mask = KeyPrefix(lengths=(positions + 1).clamp(max=cache.keys.shape[2]).to(torch.int32))
+        mask = KeyPrefix(positions=positions)
         for index, layer in enumerate(self.layers):
             keys, values = cache.keys[index], cache.values[index]
             x = layer(x, lambda attention, h: attention.step(h, keys, values, positions, mask, cos, sin))

@@ -14,7 +14,10 @@ Decode is reported beside it (``decode``): Qwen3-ASR-1.7B's GQA decoder step
 a (28, 64, 1024, 8, 128) cache, 128 steps) and Whisper-small's decoder step
 (12 layers, 12 heads x 64, batch 16, self keys 1-224, cross-attention over
 1500 frames), in algorithmic HBM GB/s (K and V of the keys each row uses,
-plus q and o).  ``secondary`` adds Whisper large-v3-turbo's encoder attention
+plus q and o), and the Qwen3 step with its prologue (per-head RMSNorm and
+rotary embedding of q and k, the cache write) fused into the decode launch,
+timed beside the unfused sequence of ops.  ``secondary`` adds Whisper
+large-v3-turbo's encoder attention
 (20 heads x 64, 1500 frames, batch 16, 32 layers).
 
 ``cpu_baseline`` times the CPU restatement of the reference's attention
@@ -203,6 +206,67 @@ class Qwen3Decode(Workload):
                 "prompt_tokens": "390 + U{10..40}", "steps": self.steps}
 
 
+class Qwen3DecodeStepFused(Qwen3Decode):
+    """The Qwen3-ASR-1.7B decoder step's attention sub-step with its prologue
+    (qwen3_asr.py:366-372, :409-432): per layer, RMSNorm and rotary embedding
+    of q (64, 16, 128) and the new key (64, 8, 128), the key/value write at
+    each row's position and the GQA attention over keys 0..position -- one
+    ``decode_append`` launch per layer.  Same cache, prompts and positions as
+    the decode workload; ``unfused_ms_per_step`` times the reference's
+    sequence of ops (norms, rotation, index writes, then the decode kernel)
+    on the same inputs.  Bytes: the old keys' K and V, the new key and
+    value (read and written), q and o."""
+
+    name = "qwen3-asr-1.7b-decode-step-fused-prologue"
+
+    def __init__(self, torch, attention, seed: int = 3, steps: int = 128) -> None:
+        super().__init__(torch, attention, seed, steps)
+        g = torch.Generator(device="cuda").manual_seed(seed + 1)
+        kv_shape = (self.layers, self.batch, self.heads_kv, self.head_dim)
+        self.k_new = torch.randn(kv_shape, generator=g, device="cuda", dtype=torch.bfloat16)
+        self.v_new = torch.randn(kv_shape, generator=g, device="cuda", dtype=torch.bfloat16)
+        self.q_norm = (torch.rand((self.layers, self.head_dim), generator=g, device="cuda") + 0.5).to(torch.bfloat16)
+        self.k_norm = (torch.rand((self.layers, self.head_dim), generator=g, device="cuda") + 0.5).to(torch.bfloat16)
+        inverse = 1.0 / (1e6 ** (torch.arange(0, self.head_dim, 2, device="cuda").float() / self.head_dim))
+        angles = torch.arange(self.cache_length, device="cuda").float()[:, None] * inverse[None, :]
+        angles = torch.cat((angles, angles), dim=-1)
+        self.cos, self.sin = angles.cos().to(torch.bfloat16), angles.sin().to(torch.bfloat16)
+        self.rows = torch.arange(self.batch, device="cuda")
+        row_bytes = 2 * self.heads_kv * self.head_dim * 2
+        qo_bytes = 2 * self.heads_q * self.head_dim * 2
+        self.step_bytes = [
+            self.layers * float(sum(row_bytes * (int(p) + t) + 2 * row_bytes + qo_bytes for p in self.prompts))
+            for t in range(self.steps)
+        ]
+        self.work_per_step = float(np.mean(self.step_bytes))
+        self.unfused = False
+
+    def run(self) -> None:
+        torch = self.torch
+        self.positions.add_(1)
+        cos, sin = self.cos[self.positions], self.sin[self.positions]
+        if not self.unfused:
+            for layer in range(self.layers):
+                self.attention.decode_append(
+                    self.q[layer], self.k_new[layer], self.v_new[layer], self.keys[layer], self.values[layer],
+                    self.positions, q_norm=self.q_norm[layer], k_norm=self.k_norm[layer], eps=1e-6,
+                    cos=cos, sin=sin, out=self.out)
+            return
+        F = torch.nn.functional
+        self.used.copy_(self.positions + 1)
+
+        def rotate(x):
+            first, second = x.chunk(2, dim=-1)
+            return x * cos[:, None, :] + torch.cat((-second, first), dim=-1) * sin[:, None, :]
+
+        for layer in range(self.layers):
+            q = rotate(F.rms_norm(self.q[layer], (self.head_dim,), self.q_norm[layer], 1e-6))
+            k = rotate(F.rms_norm(self.k_new[layer], (self.head_dim,), self.k_norm[layer], 1e-6))
+            self.keys[layer][self.rows, self.positions] = k
+            self.values[layer][self.rows, self.positions] = self.v_new[layer]
+            self.attention.decode(q, self.keys[layer], self.values[layer], seqused_k=self.used, out=self.out)
+
+
 class WhisperSmallDecoderStep(Workload):
     """Whisper-small decoder step (whisper.py:212-277): per layer, self-attention
     over the ``(16, 12, 256, 64)`` KV bucket view (keys 0..position, positions
@@ -356,7 +420,7 @@ def measure(torch, workload: Workload, steps: int, warmup: int) -> dict:
         work = workload.work_per_step
     seconds = ms / 1e3
     value = work / seconds / (1e12 if workload.unit == "TFLOP/s" else 1e9)
-    return {
+    result = {
         "workload": workload.name,
         "value": round(value, 2),
         "unit": workload.unit,
@@ -364,6 +428,13 @@ def measure(torch, workload: Workload, steps: int, warmup: int) -> dict:
         "roofline": roofline(workload, ms, work),
         "config": workload.config(),
     }
+    if isinstance(workload, Qwen3DecodeStepFused):
+        workload.unfused = True
+        unfused = time_graph(torch, workload, steps, min(warmup, workload.steps), reset=workload.reset)
+        workload.unfused = False
+        result["unfused_ms_per_step"] = round(unfused, 4)
+        result["speedup_vs_unfused"] = round(unfused / ms, 3)
+    return result
 
 
 def cpu_baseline(budget_s: float = 10.0) -> dict:
@@ -466,7 +537,8 @@ def main() -> int:
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--no-cpu-baseline", action="store_true")
-    parser.add_argument("--only", choices=["sensevoice", "turbo", "qwen3", "whisper-small", "copy"], default=None,
+    parser.add_argument("--only", choices=["sensevoice", "turbo", "qwen3", "qwen3-fused", "whisper-small", "copy"],
+                        default=None,
                         help="measure one workload only (for profiling)")
     parser.add_argument("--sweep", action="store_true",
                         help="time the encoder kernel over a table of shapes (one launch per line)")
@@ -495,6 +567,7 @@ def main() -> int:
         "sensevoice": SenseVoiceEncoder,
         "turbo": WhisperTurboEncoder,
         "qwen3": Qwen3Decode,
+        "qwen3-fused": Qwen3DecodeStepFused,
         "whisper-small": WhisperSmallDecoderStep,
         "copy": CopyCalibration,
     }
@@ -509,7 +582,7 @@ def main() -> int:
     head = measure(torch, SenseVoiceEncoder(torch, attention), args.steps, args.warmup)
     torch.cuda.empty_cache()
     decode = []
-    for cls in (Qwen3Decode, WhisperSmallDecoderStep):
+    for cls in (Qwen3Decode, Qwen3DecodeStepFused, WhisperSmallDecoderStep):
         log(f"bench: {cls.name}")
         decode.append(measure(torch, cls(torch, attention), args.steps, args.warmup))
         torch.cuda.empty_cache()

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define ASRATTN_ABI_VERSION 1
+#define ASRATTN_ABI_VERSION 2
 
 enum asrattn_status {
   ASRATTN_OK = 0,
@@ -172,6 +172,52 @@ int asrattn_decode_num_splits(const asrattn_decode_params* params);
 
 int asrattn_decode(const asrattn_decode_params* params, void* workspace,
                    size_t workspace_bytes, void* stream);
+
+/*
+ * The decoder step with its prologue fused in: the step's own key and value
+ * (one token per sequence) are appended to the cache, and q and the new key
+ * get the per-head RMSNorm and rotary embedding the reference applies
+ * before attention.  With positions[b] = p (required; seqused_k must be
+ * NULL):
+ *
+ *   q'  = rot(norm(q[b, h, :], q_norm), cos[b], sin[b])
+ *   k'  = rot(norm(k_new[b, h', :], k_norm), cos[b], sin[b])
+ *   k[b, p, h', :] = k',  v[b, p, h', :] = v_new[b, h', :]   (if p < max_len_k)
+ *   out[b, h, :] = attention of q' over cache keys j < min(p, max_len_k)
+ *                  and the new key/value
+ *
+ *   norm(x, w)[i] = x[i] / sqrt(mean(x^2) + eps) * w[i]       (w NULL: none)
+ *   rot(x, c, s)[i] = x[i] c[i] + r[i] s[i],  r = (-x[d/2:], x[:d/2])
+ *                                                        (cos NULL: none)
+ *
+ * in the cache's dtype, rounded as the reference's float32-accumulated
+ * norm and element-wise rotation round.  p_params->q is the raw q
+ * (batch, heads_q, head_dim); k/v are the cache.  Workspace as for
+ * asrattn_decode (the same size function applies).
+ *
+ * Replaces (the step path of):
+ *   q_norm/k_norm + rotate in TextAttention._project
+ *                                    src/asrback/models/qwen3_asr.py:366-372
+ *   keys[rows, positions] = k; values[rows, positions] = v, then the
+ *       attention                    src/asrback/models/qwen3_asr.py:409-432
+ *   keys.scatter_/values.scatter_ of the Whisper step (no norm, no
+ *       rotation)                    src/asrback/models/whisper.py:224-228
+ */
+typedef struct asrattn_append_params {
+  const void* k_new; /* (batch, heads_kv, head_dim), before norm and rotation */
+  const void* v_new; /* (batch, heads_kv, head_dim) */
+  int64_t kn_batch_stride, kn_head_stride;
+  int64_t vn_batch_stride, vn_head_stride;
+  const void* q_norm; /* (head_dim,) RMSNorm weights, or NULL: no norm */
+  const void* k_norm; /* (head_dim,), NULL exactly when q_norm is */
+  float eps;
+  const void* cos; /* (batch, head_dim) tables at each row's position, or NULL */
+  const void* sin; /* NULL exactly when cos is */
+  int64_t rope_batch_stride;
+} asrattn_append_params;
+
+int asrattn_decode_append(const asrattn_decode_params* params, const asrattn_append_params* append,
+                          void* workspace, size_t workspace_bytes, void* stream);
 
 /* Message of the last failed call on this thread ("" if none). */
 const char* asrattn_last_error(void);

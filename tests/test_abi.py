@@ -39,6 +39,7 @@ def test_header_declares_expected_entry_points():
     assert declared_functions() == {
         "asrattn_fwd",
         "asrattn_decode",
+        "asrattn_decode_append",
         "asrattn_decode_workspace_size",
         "asrattn_decode_num_splits",
         "asrattn_last_error",
@@ -83,12 +84,13 @@ def _c_layout(struct: str, fields: list[str]) -> dict[str, int]:
     return {k: int(v) for k, v in (line.split() for line in out.splitlines())}
 
 
-@pytest.mark.parametrize("name", ["FwdParams", "DecodeParams"])
+@pytest.mark.parametrize("name", ["FwdParams", "DecodeParams", "AppendParams"])
 def test_ctypes_structs_match_c_layout(name):
     from asrback_amd import _lib
 
     cls = getattr(_lib, name)
-    struct = {"FwdParams": "asrattn_fwd_params", "DecodeParams": "asrattn_decode_params"}[name]
+    struct = {"FwdParams": "asrattn_fwd_params", "DecodeParams": "asrattn_decode_params",
+              "AppendParams": "asrattn_append_params"}[name]
     fields = [f for f, _ in cls._fields_]
     layout = _c_layout(struct, fields)
     assert layout.pop("sizeof") == ctypes.sizeof(cls)
@@ -121,6 +123,44 @@ def test_invalid_arguments_are_reported_not_fatal(lib):
     f.scale = 0.125  # valid shape but NULL tensors
     assert lib.asrattn_fwd(ctypes.byref(f), None) == _lib.ERR_INVALID
     assert b"non-NULL" in lib.asrattn_last_error()
+
+
+def test_invalid_append_and_span_are_reported(lib):
+    """Every check below fails before any device call (the pointers are
+    stand-ins, never dereferenced)."""
+    from asrback_amd import _lib
+
+    p = _lib.DecodeParams()
+    p.batch, p.heads_q, p.heads_kv, p.head_dim, p.max_len_k = 2, 4, 2, 128, 64
+    p.dtype, p.scale = _lib.BF16, 0.125
+    p.q = p.k = p.v = p.out = 4096
+    p.q_batch_stride, p.q_head_stride = 512, 128
+    p.k_batch_stride, p.k_token_stride, p.k_head_stride = 64 * 256, 256, 128
+    p.v_batch_stride, p.v_token_stride, p.v_head_stride = 64 * 256, 256, 128
+    p.o_batch_stride, p.o_head_stride = 512, 128
+    a = _lib.AppendParams()
+    assert lib.asrattn_decode_append(ctypes.byref(p), None, None, 0, None) == _lib.ERR_INVALID
+    assert lib.asrattn_decode_append(ctypes.byref(p), ctypes.byref(a), None, 0, None) == _lib.ERR_INVALID
+    assert b"positions" in lib.asrattn_last_error()
+    p.positions = 8192
+    assert lib.asrattn_decode_append(ctypes.byref(p), ctypes.byref(a), None, 0, None) == _lib.ERR_INVALID
+    assert b"k_new" in lib.asrattn_last_error()
+    a.k_new = a.v_new = 4096
+    a.kn_batch_stride = a.vn_batch_stride = 256
+    a.kn_head_stride = a.vn_head_stride = 128
+    a.q_norm = 4096  # without k_norm
+    assert lib.asrattn_decode_append(ctypes.byref(p), ctypes.byref(a), None, 0, None) == _lib.ERR_INVALID
+    assert b"pairs" in lib.asrattn_last_error()
+    a.k_norm, a.eps = 4096, float("nan")
+    assert lib.asrattn_decode_append(ctypes.byref(p), ctypes.byref(a), None, 0, None) == _lib.ERR_INVALID
+    assert b"eps" in lib.asrattn_last_error()
+    a.eps, a.cos, a.sin, a.rope_batch_stride = 1e-6, 4096, 4104, 128  # sin misaligned
+    assert lib.asrattn_decode_append(ctypes.byref(p), ctypes.byref(a), None, 0, None) == _lib.ERR_INVALID
+    assert b"16-byte" in lib.asrattn_last_error()
+    # A sequence's keys spanning 2 GiB cannot be addressed with 32-bit offsets.
+    p.positions, p.max_len_k = 0, 1 << 23
+    assert lib.asrattn_decode(ctypes.byref(p), None, 0, None) == _lib.ERR_UNSUPPORTED
+    assert b"2 GiB" in lib.asrattn_last_error()
 
 
 def test_workspace_size_and_split_choice(lib):

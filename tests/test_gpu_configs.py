@@ -243,3 +243,85 @@ def test_errors_raise_runtime_error(ops, device):
         ops.decode(q, q[:, None].expand(2, 5, 3, 96), q[:, None].expand(2, 5, 3, 96))
     with pytest.raises(RuntimeError, match="GPU only"):
         ops.decode(q.cpu(), q.cpu()[:, None], q.cpu()[:, None])
+
+
+# --- decoder step with its prologue fused (asrattn_decode_append) ----------------
+
+
+def _ulp_diff_ok(got: torch.Tensor, want: torch.Tensor, dtype) -> bool:
+    """Equal, or (bf16) at most one unit in the last place apart on a small
+    fraction of elements: the kernel rounds where torch rounds, but sums the
+    squares in another order."""
+    if dtype == torch.float32:
+        return max_rel_err(got, want) < 1e-6
+    diff = (got.float() - want.float()).abs()
+    ulp = torch.clamp(want.float().abs(), min=1e-30) * 2.0**-7
+    return bool((diff <= ulp).all()) and float((diff > 0).float().mean()) < 0.01
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("batch,heads_q,heads_kv,splits", [(64, 16, 8, 0), (2, 4, 2, 0), (3, 8, 2, 5)])
+def test_decode_append_matches_oracle(ops, device, dtype, batch, heads_q, heads_kv, splits):
+    """Qwen3 step path fused (qwen3_asr.py:366-372, :409-432): RMSNorm and
+    rotary embedding of q and the new key, the cache write at each row's
+    position and the attention over keys 0..position, against the oracle's
+    norm/rotate (torch CPU, in the cache dtype) and SDPA.  Small batches split
+    the keys: the last split folds the new key in, the first writes it."""
+    say("decode append", dtype, batch, heads_q, heads_kv, splits)
+    hd, length, eps = 128, 1024, 1e-6
+    rng = np.random.default_rng(60 + batch)
+    positions = torch.from_numpy(rng.integers(0, 600, size=batch).astype(np.int64))
+    positions[0] = 0  # only the new key
+    q = randn(batch, heads_q, hd, seed=61, dtype=dtype)
+    k_new = randn(batch, heads_kv, hd, seed=62, dtype=dtype)
+    v_new = randn(batch, heads_kv, hd, seed=63, dtype=dtype)
+    keys = randn(batch, length, heads_kv, hd, seed=64, dtype=dtype)
+    values = randn(batch, length, heads_kv, hd, seed=65, dtype=dtype)
+    g = torch.Generator().manual_seed(66)
+    q_w = (torch.rand(hd, generator=g) + 0.5).to(dtype)
+    k_w = (torch.rand(hd, generator=g) + 0.5).to(dtype)
+    cos, sin = oa.rope_tables(1e6, hd, length, dtype)
+    cos, sin = cos[positions], sin[positions]
+    qn = oa.rotate(oa.rms_norm(q, q_w, eps), cos, sin)
+    kn = oa.rotate(oa.rms_norm(k_new, k_w, eps), cos, sin)
+    rows = torch.arange(batch)
+    keys_ref, values_ref = keys.clone(), values.clone()
+    keys_ref[rows, positions] = kn
+    values_ref[rows, positions] = v_new
+    ref = oa.qwen_step_attention(qn.float(), keys_ref.float(), values_ref.float(), oa.qwen_step_mask(positions, length))
+
+    kd, vd = keys.to(device), values.to(device)
+    out = ops.decode_append(q.to(device), k_new.to(device), v_new.to(device), kd, vd, positions.to(device),
+                            q_norm=q_w.to(device), k_norm=k_w.to(device), eps=eps, cos=cos.to(device),
+                            sin=sin.to(device), num_splits=splits)
+    assert max_rel_err(out, ref) < TOL[dtype]
+    assert _ulp_diff_ok(kd.cpu()[rows, positions], kn, dtype)
+    assert torch.equal(vd.cpu()[rows, positions], v_new)
+    untouched = torch.ones(batch, length, dtype=torch.bool)
+    untouched[rows, positions] = False
+    assert torch.equal(kd.cpu()[untouched], keys[untouched]) and torch.equal(vd.cpu()[untouched], values[untouched])
+
+
+def test_decode_append_whisper_cache_without_norm(ops, device):
+    """The Whisper step's scatter + attention (whisper.py:224-237) fused, no
+    norm or rotation, into a (batch, heads, length, head_dim) cache through
+    its transposed view."""
+    say("decode append, whisper layout")
+    rng = np.random.default_rng(70)
+    positions = torch.from_numpy(rng.integers(0, 224, size=16).astype(np.int64))
+    q = randn(16, 12, 64, seed=71, dtype=torch.bfloat16)
+    k_new = randn(16, 12, 64, seed=72, dtype=torch.bfloat16)
+    v_new = randn(16, 12, 64, seed=73, dtype=torch.bfloat16)
+    cache_k = randn(16, 12, 448, 64, seed=74, dtype=torch.bfloat16)
+    cache_v = randn(16, 12, 448, 64, seed=75, dtype=torch.bfloat16)
+    rows = torch.arange(16)
+    ref_k, ref_v = cache_k.clone(), cache_v.clone()
+    ref_k[rows, :, positions] = k_new
+    ref_v[rows, :, positions] = v_new
+    ref = oa.sdpa(q[:, :, None].float(), ref_k[:, :, :256].float(), ref_v[:, :, :256].float(),
+                  attn_mask=oa.whisper_step_mask(positions, 256))[:, :, 0]
+    kd, vd = cache_k.to(device), cache_v.to(device)
+    out = ops.decode_append(q.to(device), k_new.to(device), v_new.to(device), kd[:, :, :256].transpose(1, 2),
+                            vd[:, :, :256].transpose(1, 2), positions.to(device))
+    assert max_rel_err(out, ref) < TOL[torch.bfloat16]
+    assert torch.equal(kd.cpu(), ref_k) and torch.equal(vd.cpu(), ref_v)

@@ -166,8 +166,16 @@ def test_qwen_step_mask_forms_agree(device):
         mask = oa.qwen_step_mask(positions, 512)
         b = attn.step(x, keys.clone()[:, :512], values.clone()[:, :512], positions, mask, cos, sin)
         c = attn.step(x, keys.clone(), values.clone(), positions, KeyPrefix(lengths=lengths), cos, sin)
+        # The step mask of these very positions takes the fused kernel
+        # (norms, rotation, cache write and attention in one launch).
+        fused_keys, fused_values = keys.clone(), values.clone()
+        d = attn.step(x, fused_keys, fused_values, positions, KeyPrefix(positions=positions), cos, sin)
+        ref_keys = keys.clone()
+        attn.step(x, ref_keys, values.clone(), positions, KeyPrefix(lengths=lengths), cos, sin)
     assert max_rel_err(b, a) < 1e-6
     assert torch.equal(a, c)
+    assert max_rel_err(d, a) < 1e-5
+    assert max_rel_err(fused_keys, ref_keys) < 1e-6
 
 
 def test_qwen_step_replays_from_graph(device):
