@@ -136,6 +136,10 @@ SIGNATURES = {
         ctypes.c_int,
         [ctypes.POINTER(DecodeParams), ctypes.POINTER(AppendParams), _ptr, ctypes.c_size_t, _ptr],
     ),
+    "asrattn_choose": (
+        ctypes.c_int,
+        [_ptr, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, _ptr, _ptr, _ptr, _ptr],
+    ),
     "asrattn_decode_workspace_size": (ctypes.c_size_t, [ctypes.POINTER(DecodeParams)]),
     "asrattn_decode_num_splits": (ctypes.c_int, [ctypes.POINTER(DecodeParams)]),
     "asrattn_last_error": (ctypes.c_char_p, []),

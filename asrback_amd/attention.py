@@ -402,6 +402,37 @@ def decode_append(
     return out
 
 
+def greedy_choice(logits: Tensor, suppress: Tensor | None = None) -> tuple[Tensor, Tensor]:
+    """Greedy next token per row of float32 ``logits`` ``(rows, vocab)`` and
+    its log-probability, in one pass (``asrattn_choose``): the argmax (first
+    index among equal maxima) after setting ``suppress``-ed entries (bool or
+    uint8 ``(vocab,)``) to -inf, and ``log_softmax`` at it.  Replaces the
+    greedy path of ``whisper.py:962-974`` and ``qwen3_asr.py:1200-1210``;
+    ``logits`` is not modified.  Returns int64 tokens and float32
+    log-probabilities ``(rows,)``."""
+    if logits.dim() != 2 or logits.dtype != torch.float32:
+        raise ValueError("greedy_choice takes float32 (rows, vocab) logits")
+    if logits.stride(-1) != 1:
+        logits = logits.contiguous()  # e.g. the transposed product of Whisper's tied head
+    rows, vocab = logits.shape
+    if suppress is not None:
+        if suppress.shape != (vocab,) or suppress.dtype not in (torch.bool, torch.uint8):
+            raise ValueError(f"suppress must be a bool or uint8 ({vocab},) mask")
+        suppress = suppress.contiguous().view(torch.uint8)
+    device = _check_device(logits, suppress)
+    if device.type != "cuda":
+        raise RuntimeError("greedy_choice runs on the GPU only")
+    token = torch.empty(rows, dtype=torch.int64, device=device)
+    logprob = torch.empty(rows, dtype=torch.float32, device=device)
+    lib = _lib.load()
+    _lib.check(
+        lib.asrattn_choose(logits.data_ptr(), rows, vocab, logits.stride(0), _ptr(suppress), token.data_ptr(),
+                           logprob.data_ptr(), _stream(device)),
+        "asrattn_choose",
+    )
+    return token, logprob
+
+
 # Decode workspaces per device: one buffer serves every call on the device
 # (calls on one device run in stream order); grown buffers are kept alive
 # because graphs captured earlier still hold their addresses.

@@ -217,6 +217,20 @@ int asrattn_decode(const asrattn_decode_params* params, void* workspace, size_t 
   return run_decode(params, nullptr, workspace, workspace_bytes, stream, "asrattn_decode");
 }
 
+int asrattn_choose(const float* logits, int64_t rows, int64_t vocab, int64_t row_stride, const uint8_t* suppress,
+                   int64_t* token, float* logprob, void* stream) {
+  if (rows < 0 || rows > 0x7fffffffLL) return fail(ASRATTN_ERR_INVALID, "rows (%lld) out of range", (long long)rows);
+  // Rows are addressed with 32-bit byte offsets.
+  if (vocab < 1 || vocab >= (1LL << 29)) return fail(ASRATTN_ERR_INVALID, "vocab (%lld) out of range", (long long)vocab);
+  if (row_stride < vocab) return fail(ASRATTN_ERR_INVALID, "row_stride must be at least vocab");
+  if (rows == 0) return ok();
+  if (logits == nullptr || token == nullptr || logprob == nullptr)
+    return fail(ASRATTN_ERR_INVALID, "logits, token and logprob must be non-NULL");
+  return from_hip(asrattn::launch_choose(logits, rows, vocab, row_stride, suppress, token, logprob,
+                                         static_cast<hipStream_t>(stream)),
+                  "asrattn_choose");
+}
+
 int asrattn_decode_append(const asrattn_decode_params* params, const asrattn_append_params* append,
                           void* workspace, size_t workspace_bytes, void* stream) {
   if (append == nullptr) return fail(ASRATTN_ERR_INVALID, "append parameters must be non-NULL");

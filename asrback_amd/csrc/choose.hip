@@ -1,0 +1,179 @@
+// Greedy token choice over a row of logits in one pass: the argmax and its
+// log-probability, log_softmax(x)[argmax] = -log(sum_j exp(x_j - max)).
+//
+// One workgroup of 1024 threads per row.  Each thread reads its share in
+// rounds of eight loads issued together (16 bytes each on aligned rows), takes each round's max
+// (first index of it) and sum of exp(x - max), and folds it into its running
+// (max, index, sum), rescaling the sum when the max grows; threads then merge
+// pairwise (shuffles, then LDS) under the same rule.  Suppressed tokens count
+// as -inf (excluded from max and sum).
+//
+// Ties and NaN follow torch.argmax / log_softmax: among equal maxima the
+// first index wins; a NaN counts as the largest value (the first NaN wins)
+// and makes the row's log-probability NaN; a row of -inf picks index 0 with
+// a NaN log-probability.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace asrattn {
+namespace {
+
+constexpr int kChooseThreads = 1024;
+
+struct Best {
+  float m;    // running max (NaN if the row has a NaN)
+  int idx;    // index of the max
+  float sum;  // sum of exp(x - m) over finite x seen so far, NaN once a NaN is seen
+};
+
+// Whether candidate (x, i) replaces the running max (m, j).
+__device__ __forceinline__ bool beats(float x, int i, float m, int j) {
+  const bool xn = x != x, mn = m != m;
+  if (xn || mn) return xn && (!mn || i < j);
+  return x > m || (x == m && i < j);
+}
+
+__device__ __forceinline__ float exp_diff(float a, float b) {  // exp(a - b), 0 for a = -inf
+  return a == kNegInf ? 0.f : fast_exp2((a - b) * kLog2e);
+}
+
+__device__ __forceinline__ void add(Best& s, float x, int i) {
+  if (x != x) {  // NaN: the max (first one) and a NaN sum
+    if (s.m == s.m || i < s.idx) {
+      s.m = x;
+      s.idx = i;
+    }
+    s.sum = x;
+    return;
+  }
+  if (beats(x, i, s.m, s.idx)) {
+    if (s.m == s.m) s.sum = s.sum * exp_diff(s.m, x);  // rescale (0 while m is -inf and sum is 0)
+    s.m = x;
+    s.idx = i;
+  }
+  s.sum += exp_diff(x, s.m);
+}
+
+__device__ __forceinline__ Best merge(const Best& a, const Best& b) {
+  Best r;
+  const bool take_b = beats(b.m, b.idx, a.m, a.idx);
+  r.m = take_b ? b.m : a.m;
+  r.idx = take_b ? b.idx : a.idx;
+  if (r.m != r.m) {
+    r.sum = r.m;
+  } else {
+    r.sum = a.sum * exp_diff(a.m, r.m) + b.sum * exp_diff(b.m, r.m);
+  }
+  return r;
+}
+
+// Loads per thread per round: a round's loads all issue before any is
+// consumed (the rounds are latency-bound otherwise).
+constexpr int kChunk = 8;
+
+// Q = 4: 16-byte loads over the row's whole groups of four (16-byte aligned
+// rows), the at most three last elements one by one; Q = 1: 4-byte loads.
+// The resources end exactly at the row's (and the mask's) last element, so
+// no load straddles an end; lanes past it read zeros, excluded by index.
+template <int Q>
+__global__ __launch_bounds__(kChooseThreads) void choose_kernel(const float* logits, int64_t vocab, int64_t row_stride,
+                                                                const uint8_t* suppress, int64_t* token,
+                                                                float* logprob) {
+  const int64_t row = blockIdx.x;
+  const float* x = logits + row * row_stride;
+  const int tid = threadIdx.x;
+  Best s{kNegInf, 0x7fffffff, 0.f};
+  const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(x, (uint32_t)(vocab * 4));
+  const __amdgpu_buffer_rsrc_t sr = buffer_rsrc(suppress != nullptr ? suppress : reinterpret_cast<const uint8_t*>(x),
+                                                suppress != nullptr ? (uint32_t)vocab : 0u);
+  const int64_t groups = vocab / Q;
+  for (int64_t c0 = 0; c0 < groups; c0 += (int64_t)kChooseThreads * kChunk) {
+    float xs[kChunk][Q];
+    uint32_t sup[kChunk];
+#pragma unroll
+    for (int k = 0; k < kChunk; ++k) {
+      const uint32_t c = (uint32_t)(c0 + tid + k * kChooseThreads);
+      if constexpr (Q == 4) {
+        const uint4 v = buffer_load16(xr, c * 16u);
+        xs[k][0] = __uint_as_float(v.x);
+        xs[k][1] = __uint_as_float(v.y);
+        xs[k][2] = __uint_as_float(v.z);
+        xs[k][3] = __uint_as_float(v.w);
+        sup[k] = __builtin_amdgcn_raw_buffer_load_b32(sr, c * 4u, 0, 0);
+      } else {
+        xs[k][0] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(xr, c * 4u, 0, 0));
+        sup[k] = __builtin_amdgcn_raw_buffer_load_b8(sr, c, 0, 0);
+      }
+    }
+    // The round's max and first index of it, then its sum against that max.
+    Best cb{kNegInf, 0x7fffffff, 0.f};
+#pragma unroll
+    for (int k = 0; k < kChunk; ++k) {
+      const int64_t c = c0 + tid + k * kChooseThreads;
+#pragma unroll
+      for (int q = 0; q < Q; ++q) {
+        const bool live = c < groups && ((sup[k] >> (8 * q)) & 0xffu) == 0;
+        xs[k][q] = live ? xs[k][q] : kNegInf;
+        const int i = (int)(c * Q + q);
+        if (beats(xs[k][q], i, cb.m, cb.idx)) {
+          cb.m = xs[k][q];
+          cb.idx = i;
+        }
+      }
+    }
+    if (cb.m != cb.m) {
+      cb.sum = cb.m;  // a NaN is the round's max, and its sum is NaN
+    } else {
+#pragma unroll
+      for (int k = 0; k < kChunk; ++k)
+#pragma unroll
+        for (int q = 0; q < Q; ++q) cb.sum += exp_diff(xs[k][q], cb.m);
+    }
+    s = merge(s, cb);
+  }
+  for (int64_t i = groups * Q + tid; i < vocab; i += kChooseThreads)
+    add(s, (suppress != nullptr && suppress[i]) ? kNegInf : x[i], (int)i);
+  // Threads that saw nothing (vocab < threads) hold (-inf, INT_MAX, 0):
+  // they lose every comparison and add nothing.
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    Best o;
+    o.m = __shfl_xor(s.m, off, 64);
+    o.idx = __shfl_xor(s.idx, off, 64);
+    o.sum = __shfl_xor(s.sum, off, 64);
+    s = merge(s, o);
+  }
+  __shared__ Best part[kChooseThreads / 64];
+  if ((tid & 63) == 0) part[tid >> 6] = s;
+  __syncthreads();
+  if (tid == 0) {
+    Best r = part[0];
+#pragma unroll
+    for (int w = 1; w < kChooseThreads / 64; ++w) r = merge(r, part[w]);
+    // A row of -inf: torch.argmax gives index 0, log_softmax NaN.
+    if (r.m == kNegInf) {
+      r.idx = 0;
+      r.sum = __builtin_nanf("");
+    }
+    token[row] = r.idx;
+    logprob[row] = r.sum != r.sum ? r.sum : -logf(r.sum);
+  }
+}
+
+}  // namespace
+
+hipError_t launch_choose(const float* logits, int64_t rows, int64_t vocab, int64_t row_stride, const uint8_t* suppress,
+                         int64_t* token, float* logprob, hipStream_t stream) {
+  // 16-byte loads need 16-byte aligned rows (and 4-byte aligned mask words).
+  const bool vec = (reinterpret_cast<uintptr_t>(logits) & 15u) == 0 && row_stride % 4 == 0 &&
+                   (suppress == nullptr || (reinterpret_cast<uintptr_t>(suppress) & 3u) == 0);
+  if (vec)
+    hipLaunchKernelGGL(choose_kernel<4>, dim3((unsigned)rows), dim3(kChooseThreads), 0, stream, logits, vocab,
+                       row_stride, suppress, token, logprob);
+  else
+    hipLaunchKernelGGL(choose_kernel<1>, dim3((unsigned)rows), dim3(kChooseThreads), 0, stream, logits, vocab,
+                       row_stride, suppress, token, logprob);
+  return hipGetLastError();
+}
+
+}  // namespace asrattn

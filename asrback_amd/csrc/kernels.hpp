@@ -23,6 +23,11 @@ bool decode_supported(int dtype, int head_dim, int group);
 hipError_t launch_fwd_ring(const asrattn_fwd_params& p, hipStream_t stream);
 bool fwd_ring_supported(const asrattn_fwd_params& p);
 
+// Greedy choice per row of fp32 logits: argmax (first index on ties) and its
+// log-probability; suppress (uint8 per vocabulary entry) may be null.
+hipError_t launch_choose(const float* logits, int64_t rows, int64_t vocab, int64_t row_stride, const uint8_t* suppress,
+                         int64_t* token, float* logprob, hipStream_t stream);
+
 // Multi-row forward on the vector ALUs (fp32 or bf16, head_dim 64 or 128):
 // the fp32 path, the fallback for bf16 layouts the matrix-core kernel does
 // not address, and the reference-precision check of that kernel.

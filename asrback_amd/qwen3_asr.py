@@ -31,7 +31,7 @@ import torch
 import torch.nn.functional as F
 from torch import Tensor, nn
 
-from .attention import KeyPrefix, decode, decode_append, varlen_attn
+from .attention import KeyPrefix, decode, decode_append, greedy_choice, varlen_attn
 from .transcription import CapturedGraph, to_device
 
 # Positions per row of the KV cache (qwen3_asr.py:57-59).
@@ -312,7 +312,11 @@ class DecodeState:
 
 def choose(logits: Tensor, temperatures: Tensor | None = None) -> tuple[Tensor, Tensor]:
     """Next token per row -- greedy, or sampled where the row's temperature is
-    positive -- and its log-probability (``qwen3_asr.py:1200-1210``)."""
+    positive -- and its log-probability (``qwen3_asr.py:1200-1210``).  All
+    greedy over fp32 logits on the GPU: one fused pass
+    (:func:`~asrback_amd.attention.greedy_choice`)."""
+    if temperatures is None and logits.is_cuda and logits.dtype == torch.float32 and logits.dim() == 2:
+        return greedy_choice(logits)
     token = logits.argmax(dim=-1)
     if temperatures is not None:
         scaled = logits / temperatures.clamp(min=1e-6)[:, None]

@@ -30,7 +30,7 @@ import torch
 import torch.nn.functional as F
 from torch import Tensor, nn
 
-from .attention import KeyPrefix, sdpa
+from .attention import KeyPrefix, greedy_choice, sdpa
 from .transcription import CapturedGraph, to_device
 
 # Self-attention lengths with their own graph, besides max_target_positions
@@ -313,7 +313,11 @@ class DecodeState:
 
 def choose(logits: Tensor, suppress: Tensor) -> tuple[Tensor, Tensor]:
     """Greedy next token per row and its log-probability (``whisper.py:962-974``,
-    temperature 0)."""
+    temperature 0).  fp32 logits on the GPU take one fused pass
+    (:func:`~asrback_amd.attention.greedy_choice`; ``logits`` stays
+    unmodified), others the reference's ops."""
+    if logits.is_cuda and logits.dtype == torch.float32 and logits.dim() == 2 and suppress.dim() == 1:
+        return greedy_choice(logits, suppress)
     logits.masked_fill_(suppress, -math.inf)
     token = logits.argmax(dim=-1)
     logprob = F.log_softmax(logits, dim=-1).gather(1, token[:, None]).squeeze(1)

@@ -16,7 +16,8 @@ a (28, 64, 1024, 8, 128) cache, 128 steps) and Whisper-small's decoder step
 1500 frames), in algorithmic HBM GB/s (K and V of the keys each row uses,
 plus q and o), and the Qwen3 step with its prologue (per-head RMSNorm and
 rotary embedding of q and k, the cache write) fused into the decode launch,
-timed beside the unfused sequence of ops.  ``secondary`` adds Whisper
+timed beside the unfused sequence of ops, and the greedy token choice over
+Qwen3's (64, 151936) logits in one pass.  ``secondary`` adds Whisper
 large-v3-turbo's encoder attention
 (20 heads x 64, 1500 frames, batch 16, 32 layers).
 
@@ -267,6 +268,44 @@ class Qwen3DecodeStepFused(Qwen3Decode):
             self.attention.decode(q, self.keys[layer], self.values[layer], seqused_k=self.used, out=self.out)
 
 
+class GreedyChoice(Workload):
+    """The greedy token choice of a Qwen3-ASR-1.7B decoder step
+    (qwen3_asr.py:1200-1210): argmax and log_softmax at it over fp32 logits
+    (64, 151936), one fused pass; ``unfused_ms_per_step`` times torch's
+    argmax, log_softmax and gather on the same logits.  Bytes: the logits
+    read once, tokens and log-probabilities written."""
+
+    name = "qwen3-asr-1.7b-greedy-choice"
+    unit = "GB/s"
+    bound = "hbm"
+    kernel = "choose_kernel"
+
+    def __init__(self, torch, attention, seed: int = 5) -> None:
+        self.torch = torch
+        self.rows, self.vocab = 64, 151936
+        g = torch.Generator(device="cuda").manual_seed(seed)
+        self.logits = torch.randn((self.rows, self.vocab), generator=g, device="cuda") * 4
+        self.token = torch.empty(self.rows, dtype=torch.long, device="cuda")
+        self.logprob = torch.empty(self.rows, device="cuda")
+        self.attention = attention
+        self.launches = 1
+        self.work_per_step = float(self.rows * self.vocab * 4 + self.rows * 12)
+        self.unfused = False
+
+    def run(self) -> None:
+        torch = self.torch
+        if not self.unfused:
+            token, logprob = self.attention.greedy_choice(self.logits)
+        else:
+            token = self.logits.argmax(dim=-1)
+            logprob = torch.log_softmax(self.logits, dim=-1).gather(1, token[:, None]).squeeze(1)
+        self.token.copy_(token)
+        self.logprob.copy_(logprob)
+
+    def config(self) -> dict:
+        return {"workload": self.name, "rows": self.rows, "vocab": self.vocab, "dtype": "float32 logits"}
+
+
 class WhisperSmallDecoderStep(Workload):
     """Whisper-small decoder step (whisper.py:212-277): per layer, self-attention
     over the ``(16, 12, 256, 64)`` KV bucket view (keys 0..position, positions
@@ -428,6 +467,12 @@ def measure(torch, workload: Workload, steps: int, warmup: int) -> dict:
         "roofline": roofline(workload, ms, work),
         "config": workload.config(),
     }
+    if isinstance(workload, GreedyChoice):
+        workload.unfused = True
+        unfused = time_graph(torch, workload, steps, warmup)
+        workload.unfused = False
+        result["unfused_ms_per_step"] = round(unfused, 4)
+        result["speedup_vs_unfused"] = round(unfused / ms, 3)
     if isinstance(workload, Qwen3DecodeStepFused):
         workload.unfused = True
         unfused = time_graph(torch, workload, steps, min(warmup, workload.steps), reset=workload.reset)
@@ -537,7 +582,8 @@ def main() -> int:
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--no-cpu-baseline", action="store_true")
-    parser.add_argument("--only", choices=["sensevoice", "turbo", "qwen3", "qwen3-fused", "whisper-small", "copy"],
+    parser.add_argument("--only", choices=["sensevoice", "turbo", "qwen3", "qwen3-fused", "whisper-small", "choice",
+                                           "copy"],
                         default=None,
                         help="measure one workload only (for profiling)")
     parser.add_argument("--sweep", action="store_true",
@@ -568,6 +614,7 @@ def main() -> int:
         "turbo": WhisperTurboEncoder,
         "qwen3": Qwen3Decode,
         "qwen3-fused": Qwen3DecodeStepFused,
+        "choice": GreedyChoice,
         "whisper-small": WhisperSmallDecoderStep,
         "copy": CopyCalibration,
     }
@@ -582,7 +629,7 @@ def main() -> int:
     head = measure(torch, SenseVoiceEncoder(torch, attention), args.steps, args.warmup)
     torch.cuda.empty_cache()
     decode = []
-    for cls in (Qwen3Decode, Qwen3DecodeStepFused, WhisperSmallDecoderStep):
+    for cls in (Qwen3Decode, Qwen3DecodeStepFused, WhisperSmallDecoderStep, GreedyChoice):
         log(f"bench: {cls.name}")
         decode.append(measure(torch, cls(torch, attention), args.steps, args.warmup))
         torch.cuda.empty_cache()

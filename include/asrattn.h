@@ -219,6 +219,27 @@ typedef struct asrattn_append_params {
 int asrattn_decode_append(const asrattn_decode_params* params, const asrattn_append_params* append,
                           void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * Greedy next token per row of float32 logits, in one pass:
+ *
+ *   token[r]   = argmax_j x[r, j]       (first index among equal maxima)
+ *   logprob[r] = log_softmax(x[r])[token[r]] = -log(sum_j exp(x[r, j] - max))
+ *
+ * with x[r, j] = -inf where suppress[j] != 0 (suppress: uint8[vocab], or
+ * NULL).  NaN counts as the largest value and makes the row's logprob NaN;
+ * a row of -inf gives token 0 and a NaN logprob (torch.argmax and
+ * log_softmax behave the same).  logits row r starts at logits +
+ * r*row_stride (row_stride >= vocab); token is int64[rows], logprob
+ * float32[rows].  1 <= vocab < 2^29.
+ *
+ * Replaces the greedy path of:
+ *   logits.masked_fill_(suppress, -inf); argmax; log_softmax; gather
+ *                                    src/asrback/models/whisper.py:962-974
+ *   argmax; log_softmax; gather      src/asrback/models/qwen3_asr.py:1200-1210
+ */
+int asrattn_choose(const float* logits, int64_t rows, int64_t vocab, int64_t row_stride, const uint8_t* suppress,
+                   int64_t* token, float* logprob, void* stream);
+
 /* Message of the last failed call on this thread ("" if none). */
 const char* asrattn_last_error(void);
 

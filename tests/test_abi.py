@@ -40,6 +40,7 @@ def test_header_declares_expected_entry_points():
         "asrattn_fwd",
         "asrattn_decode",
         "asrattn_decode_append",
+        "asrattn_choose",
         "asrattn_decode_workspace_size",
         "asrattn_decode_num_splits",
         "asrattn_last_error",

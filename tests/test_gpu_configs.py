@@ -325,3 +325,70 @@ def test_decode_append_whisper_cache_without_norm(ops, device):
                             vd[:, :, :256].transpose(1, 2), positions.to(device))
     assert max_rel_err(out, ref) < TOL[torch.bfloat16]
     assert torch.equal(kd.cpu(), ref_k) and torch.equal(vd.cpu(), ref_v)
+
+
+# --- greedy choice (asrattn_choose) ---------------------------------------------
+
+
+def _torch_choice(logits: torch.Tensor, suppress: torch.Tensor | None):
+    x = logits.clone()
+    if suppress is not None:
+        x.masked_fill_(suppress, float("-inf"))
+    token = x.argmax(dim=-1)
+    return token, torch.log_softmax(x, dim=-1).gather(1, token[:, None]).squeeze(1)
+
+
+@pytest.mark.parametrize("vocab", [1000, 51865, 151936])
+def test_greedy_choice_matches_torch(ops, device, vocab):
+    """argmax + log_softmax at it in one pass (whisper.py:962-974,
+    qwen3_asr.py:1200-1210) against torch on the CPU: tokens exact,
+    log-probabilities to 1e-5; rows with ties, a suppress mask, NaN and
+    all -inf rows; odd vocabularies take the element-wise path."""
+    say("greedy choice", vocab)
+    g = torch.Generator().manual_seed(80 + vocab % 97)
+    logits = torch.randn(9, vocab, generator=g) * 4
+    logits[1, 7] = logits[1, vocab - 3] = logits[1].max() + 1.0  # tie: first index wins
+    logits[2, :] = 0.5  # all equal
+    logits[3, 5] = float("nan")
+    logits[3, 9] = float("nan")
+    logits[4, :] = float("-inf")
+    logits[5, : vocab // 2] = float("-inf")
+    suppress = torch.zeros(vocab, dtype=torch.bool)
+    suppress[torch.randperm(vocab, generator=g)[: vocab // 10]] = True
+    suppress[int(logits[6].argmax())] = True  # the row's max is suppressed
+    for mask in (None, suppress):
+        want_t, want_p = _torch_choice(logits, mask)
+        got_t, got_p = ops.greedy_choice(logits.to(device), None if mask is None else mask.to(device))
+        got_t, got_p = got_t.cpu(), got_p.cpu()
+        assert torch.equal(got_t, want_t), (got_t, want_t)
+        nan = torch.isnan(want_p)
+        assert torch.equal(torch.isnan(got_p), nan)
+        assert torch.allclose(got_p[~nan], want_p[~nan], rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("offset,vocab,stride", [(1, 1000, 1003), (0, 1001, 1004), (0, 4093, 4096)])
+def test_greedy_choice_strided_rows(ops, device, offset, vocab, stride):
+    """Rows inside a wider buffer: unaligned (4-byte loads), and aligned with
+    a vocabulary that is not a multiple of four (16-byte loads plus the
+    element-wise tail)."""
+    buf = randn(6, stride, seed=85 + vocab) * 3
+    buf[2, offset + vocab - 1] = 50.0  # the max sits in the tail
+    mask = torch.zeros(vocab, dtype=torch.bool)
+    mask[vocab - 2] = True
+    for m in (None, mask):
+        want_t, want_p = _torch_choice(buf[:, offset:offset + vocab], m)
+        got_t, got_p = ops.greedy_choice(buf.to(device)[:, offset:offset + vocab], None if m is None else m.to(device))
+        assert torch.equal(got_t.cpu(), want_t)
+        assert torch.allclose(got_p.cpu(), want_p, rtol=1e-5, atol=1e-5)
+
+
+def test_greedy_choice_column_major_logits(ops, device):
+    """Logits of a transposed product (Whisper's head computes (W h^T)^T)."""
+    w = randn(700, 64, seed=86)
+    h = randn(5, 64, seed=87)
+    logits = (w.to(device) @ h.to(device).T).T
+    assert logits.stride(-1) != 1
+    want_t, want_p = _torch_choice(logits.cpu(), None)
+    got_t, got_p = ops.greedy_choice(logits)
+    assert torch.equal(got_t.cpu(), want_t)
+    assert torch.allclose(got_p.cpu(), want_p, rtol=1e-5, atol=1e-5)
