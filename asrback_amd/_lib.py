@@ -19,7 +19,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must be imported before the library; see above)
 
 LIBRARY = Path(__file__).resolve().with_name("libasrattn.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 # enum asrattn_status / asrattn_dtype / asrattn_causal
 OK = 0
@@ -125,9 +125,23 @@ class AppendParams(ctypes.Structure):
     ]
 
 
+class FsmnParams(ctypes.Structure):
+    """``asrattn_fsmn_params``."""
+
+    _fields_ = [
+        ("weight", _ptr),
+        ("bias", _ptr),
+        ("memory", _ptr),
+        ("m_batch_stride", _i64),
+        ("m_token_stride", _i64),
+        ("kernel_size", _i32),
+    ]
+
+
 # Every symbol include/asrattn.h declares, with (restype, argtypes).
 SIGNATURES = {
     "asrattn_fwd": (ctypes.c_int, [ctypes.POINTER(FwdParams), _ptr]),
+    "asrattn_fwd_fsmn": (ctypes.c_int, [ctypes.POINTER(FwdParams), ctypes.POINTER(FsmnParams), _ptr]),
     "asrattn_decode": (
         ctypes.c_int,
         [ctypes.POINTER(DecodeParams), _ptr, ctypes.c_size_t, _ptr],

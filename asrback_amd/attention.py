@@ -19,6 +19,11 @@ Three entry points cover every attention call of the reference:
   strides (the Whisper ``(B, H, L, D)`` and Qwen3 ``(B, L, H_kv, D)``
   caches).
 
+The fused neighbours of those calls: :func:`flash` (the multi-row kernel
+itself), :func:`flash_fsmn` (SenseVoice attention plus its FSMN memory),
+:func:`decode_append` (the decoder step with its norms, rotation and cache
+write) and :func:`greedy_choice` (argmax and its log-probability).
+
 The reference's masks are all prefix masks: each query row sees keys
 ``0 .. n-1`` (optionally causal on top).  General boolean masks are not
 supported.
@@ -129,28 +134,23 @@ def _int32(t: Tensor | None, name: str) -> Tensor | None:
     return t.contiguous()
 
 
-def flash(
+def _fwd_params(
     q: Tensor,
     k: Tensor,
     v: Tensor,
-    *,
-    out: Tensor | None = None,
-    causal: int = _lib.CAUSAL_NONE,
-    cu_seqlens_q: Tensor | None = None,
-    cu_seqlens_k: Tensor | None = None,
-    max_len_q: int | None = None,
-    max_len_k: int | None = None,
-    seqused_k: Tensor | None = None,
-    scale: float | None = None,
-    force_valu: bool = False,
-) -> Tensor:
-    """Multi-row attention (``asrattn_fwd``).
-
-    Padded layout: ``q`` ``(batch, len_q, heads_q, head_dim)``, ``k``/``v``
-    ``(batch, len_k, heads_kv, head_dim)``; packed layout (``cu_seqlens_*``
-    given): ``(tokens, heads, head_dim)``.  Returns ``out`` in ``q``'s layout
-    (a new contiguous tensor unless ``out`` is given).
-    """
+    out: Tensor | None,
+    causal: int,
+    cu_seqlens_q: Tensor | None,
+    cu_seqlens_k: Tensor | None,
+    max_len_q: int | None,
+    max_len_k: int | None,
+    seqused_k: Tensor | None,
+    scale: float | None,
+    force_valu: bool,
+) -> tuple[_lib.FwdParams, Tensor, torch.device, tuple]:
+    """``asrattn_fwd_params`` for :func:`flash`; returns them with ``out``,
+    the device and the tensors the parameters point into (kept alive until
+    the launch)."""
     dtype = _dtype_code(q, k, v)
     packed = cu_seqlens_q is not None
     if packed != (cu_seqlens_k is not None):
@@ -217,9 +217,94 @@ def flash(
     params.dtype = dtype
     params.scale = 1.0 / math.sqrt(head_dim) if scale is None else scale
     params.flags = _lib.FWD_FORCE_VALU if force_valu else 0
+    return params, out, device, (q, k, v, cu_seqlens_q, cu_seqlens_k, seqused_k)
+
+
+def flash(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    *,
+    out: Tensor | None = None,
+    causal: int = _lib.CAUSAL_NONE,
+    cu_seqlens_q: Tensor | None = None,
+    cu_seqlens_k: Tensor | None = None,
+    max_len_q: int | None = None,
+    max_len_k: int | None = None,
+    seqused_k: Tensor | None = None,
+    scale: float | None = None,
+    force_valu: bool = False,
+) -> Tensor:
+    """Multi-row attention (``asrattn_fwd``).
+
+    Padded layout: ``q`` ``(batch, len_q, heads_q, head_dim)``, ``k``/``v``
+    ``(batch, len_k, heads_kv, head_dim)``; packed layout (``cu_seqlens_*``
+    given): ``(tokens, heads, head_dim)``.  Returns ``out`` in ``q``'s layout
+    (a new contiguous tensor unless ``out`` is given).
+    """
+    params, out, device, keep = _fwd_params(
+        q, k, v, out, causal, cu_seqlens_q, cu_seqlens_k, max_len_q, max_len_k, seqused_k, scale, force_valu
+    )
     lib = _lib.load()
     _lib.check(lib.asrattn_fwd(ctypes.byref(params), _stream(device)), "asrattn_fwd")
+    del keep
     return out
+
+
+def flash_fsmn(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    weight: Tensor,
+    *,
+    seqused_k: Tensor | None = None,
+    bias: Tensor | None = None,
+    out: Tensor | None = None,
+    memory: Tensor | None = None,
+    scale: float | None = None,
+    force_valu: bool = False,
+) -> tuple[Tensor, Tensor]:
+    """SAN-M self-attention and its FSMN memory in one call
+    (``asrattn_fwd_fsmn``; ``sensevoice.py:97-135``).
+
+    ``q``/``k``/``v`` ``(batch, frames, heads, head_dim)`` (views of the
+    fused projection), ``seqused_k`` the int32 frame counts (or None: every
+    frame is real), ``weight`` the depthwise Conv1d weight ``(C, 1, K)`` or
+    ``(C, K)`` with ``C = heads * head_dim``.  Returns ``(out, memory)``,
+    ``memory`` ``(batch, frames, C)`` = the reference's FSMN memory plus
+    ``bias`` (if given) on every row.
+    """
+    if q.shape != k.shape or q.shape != v.shape:
+        raise ValueError("the FSMN path needs q, k and v of one shape (batch, frames, heads, head_dim)")
+    batch, frames, heads, head_dim = q.shape
+    channels = heads * head_dim
+    weight = weight.reshape(weight.shape[0], weight.shape[-1]) if weight.dim() == 3 else weight
+    if weight.dim() != 2 or weight.shape[0] != channels:
+        raise ValueError(f"weight must be ({channels}, 1, K) or ({channels}, K), got {tuple(weight.shape)}")
+    weight = weight.contiguous()
+    if bias is not None:
+        if bias.shape != (channels,):
+            raise ValueError(f"bias must be ({channels},), got {tuple(bias.shape)}")
+        bias = bias.contiguous()
+    _dtype_code(q, weight, *(() if bias is None else (bias,)))
+    if memory is None:
+        memory = torch.empty((batch, frames, channels), dtype=q.dtype, device=q.device)
+    elif memory.shape != (batch, frames, channels) or memory.dtype != q.dtype or memory.stride(-1) != 1:
+        raise ValueError("memory must be a (batch, frames, channels) tensor of q's dtype with unit channel stride")
+    params, out, device, keep = _fwd_params(
+        q, k, v, out, _lib.CAUSAL_NONE, None, None, None, None, seqused_k, scale, force_valu
+    )
+    _check_device(q, weight, bias, memory)
+    f = _lib.FsmnParams()
+    f.weight, f.bias, f.memory = weight.data_ptr(), _ptr(bias), memory.data_ptr()
+    f.m_batch_stride, f.m_token_stride = memory.stride(0), memory.stride(1)
+    f.kernel_size = weight.shape[1]
+    lib = _lib.load()
+    _lib.check(
+        lib.asrattn_fwd_fsmn(ctypes.byref(params), ctypes.byref(f), _stream(device)), "asrattn_fwd_fsmn"
+    )
+    del keep
+    return out, memory
 
 
 def _decode_params(

@@ -121,7 +121,12 @@ const char* asrattn_last_error(void) { return g_last_error.c_str(); }
 
 int asrattn_abi_version(void) { return ASRATTN_ABI_VERSION; }
 
-int asrattn_fwd(const asrattn_fwd_params* params, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// Argument checks of asrattn_fwd; *empty is set when there is nothing to do.
+int check_fwd(const asrattn_fwd_params* params, bool* empty) {
   if (params == nullptr) return fail(ASRATTN_ERR_INVALID, "params is NULL");
   const asrattn_fwd_params& p = *params;
   int rc = check_common(p.dtype, p.heads_q, p.heads_kv, p.head_dim, p.scale);
@@ -133,7 +138,8 @@ int asrattn_fwd(const asrattn_fwd_params* params, void* stream) {
     return fail(ASRATTN_ERR_INVALID, "causal must be 0, 1 or 2, got %d", p.causal);
   if ((p.cu_seqlens_q == nullptr) != (p.cu_seqlens_k == nullptr))
     return fail(ASRATTN_ERR_INVALID, "cu_seqlens_q and cu_seqlens_k must both be set or both be NULL");
-  if (p.batch == 0 || p.max_len_q == 0) return ok();
+  *empty = p.batch == 0 || p.max_len_q == 0;
+  if (*empty) return ASRATTN_OK;
   if (p.q == nullptr || p.k == nullptr || p.v == nullptr || p.out == nullptr)
     return fail(ASRATTN_ERR_INVALID, "q, k, v and out must be non-NULL");
   if (!vec_aligned(p.q, p.dtype, {p.q_batch_stride, p.q_token_stride, p.q_head_stride}) ||
@@ -143,11 +149,73 @@ int asrattn_fwd(const asrattn_fwd_params* params, void* stream) {
     return fail(ASRATTN_ERR_INVALID,
                 "q, k, v and out need 16-byte aligned pointers and strides that are multiples of 16 bytes");
   const bool generic = (p.flags & ASRATTN_FWD_FORCE_VALU) != 0;
-  if (!generic && asrattn::fwd_ring_supported(p))
-    return from_hip(asrattn::launch_fwd_ring(p, static_cast<hipStream_t>(stream)), "asrattn_fwd (ring)");
-  if (asrattn::fwd_valu_supported(p.dtype, p.head_dim))
-    return from_hip(asrattn::launch_fwd_valu(p, static_cast<hipStream_t>(stream)), "asrattn_fwd (valu)");
-  return fail(ASRATTN_ERR_UNSUPPORTED, "no forward kernel for head_dim %d (supported: 64, 128)", p.head_dim);
+  if ((generic || !asrattn::fwd_ring_supported(p)) && !asrattn::fwd_valu_supported(p.dtype, p.head_dim))
+    return fail(ASRATTN_ERR_UNSUPPORTED, "no forward kernel for head_dim %d (supported: 64, 128)", p.head_dim);
+  return ASRATTN_OK;
+}
+
+// The attention launch of asrattn_fwd / asrattn_fwd_fsmn; fsmn (or null) is
+// fused into the matrix-core kernel, else launched after the attention.
+int run_fwd(const asrattn_fwd_params& p, const asrattn::FsmnArgs* fsmn, void* stream, const char* name) {
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool generic = (p.flags & ASRATTN_FWD_FORCE_VALU) != 0;
+  hipError_t err;
+  if (!generic && asrattn::fwd_ring_supported(p)) {
+    const bool fused = fsmn != nullptr && fsmn->kernel_size <= asrattn::kFsmnFusedKernel;
+    err = asrattn::launch_fwd_ring(p, fused ? fsmn : nullptr, s);
+    if (fused || fsmn == nullptr || err != hipSuccess) return from_hip(err, name);
+  } else {
+    err = asrattn::launch_fwd_valu(p, s);
+    if (fsmn == nullptr || err != hipSuccess) return from_hip(err, name);
+  }
+  return from_hip(asrattn::launch_fsmn(p, *fsmn, s), name);
+}
+
+}  // namespace
+
+extern "C" {
+
+int asrattn_fwd(const asrattn_fwd_params* params, void* stream) {
+  bool empty = false;
+  const int rc = check_fwd(params, &empty);
+  if (rc != ASRATTN_OK) return rc;
+  if (empty) return ok();
+  return run_fwd(*params, nullptr, stream, "asrattn_fwd");
+}
+
+int asrattn_fwd_fsmn(const asrattn_fwd_params* params, const asrattn_fsmn_params* fsmn, void* stream) {
+  if (fsmn == nullptr) return fail(ASRATTN_ERR_INVALID, "fsmn parameters must be non-NULL");
+  bool empty = false;
+  const int rc = check_fwd(params, &empty);
+  if (rc != ASRATTN_OK) return rc;
+  const asrattn_fwd_params& p = *params;
+  const asrattn_fsmn_params& f = *fsmn;
+  if (p.causal != ASRATTN_CAUSAL_NONE || p.cu_seqlens_q != nullptr || p.heads_q != p.heads_kv ||
+      p.max_len_q != p.max_len_k)
+    return fail(ASRATTN_ERR_INVALID,
+                "the FSMN memory needs the padded, non-causal layout with max_len_q == max_len_k and heads_q == "
+                "heads_kv");
+  if (f.kernel_size < 1 || f.kernel_size > asrattn::kFsmnMaxKernel)
+    return fail(ASRATTN_ERR_UNSUPPORTED, "FSMN kernel_size must be in [1, %d], got %d", asrattn::kFsmnMaxKernel,
+                f.kernel_size);
+  if (p.head_dim != 64 && p.head_dim != 128)
+    return fail(ASRATTN_ERR_UNSUPPORTED, "FSMN memory for head_dim %d (supported: 64, 128)", p.head_dim);
+  if (empty) return ok();
+  if (f.weight == nullptr || f.memory == nullptr)
+    return fail(ASRATTN_ERR_INVALID, "the FSMN weight and memory must be non-NULL");
+  if (!vec_aligned(f.memory, p.dtype, {f.m_batch_stride, f.m_token_stride}))
+    return fail(ASRATTN_ERR_INVALID, "memory needs a 16-byte aligned pointer and strides that are multiples of 16 bytes");
+  const size_t es = (size_t)elem_bytes(p.dtype);
+  if ((reinterpret_cast<uintptr_t>(f.weight) % es) != 0 ||
+      (f.bias != nullptr && (reinterpret_cast<uintptr_t>(f.bias) % es) != 0))
+    return fail(ASRATTN_ERR_INVALID, "weight and bias must be aligned to their element size");
+  // Value and memory rows are addressed with 32-bit byte offsets, up to a
+  // block of rows past the end.
+  if (((long long)p.max_len_k + 160) * p.v_token_stride * (long long)es >= (1LL << 31) ||
+      ((long long)p.max_len_q + 160) * f.m_token_stride * (long long)es >= (1LL << 31))
+    return fail(ASRATTN_ERR_UNSUPPORTED, "one sequence's values or memory span 2 GiB or more");
+  const asrattn::FsmnArgs a{f.weight, f.bias, f.memory, f.m_batch_stride, f.m_token_stride, f.kernel_size};
+  return run_fwd(p, &a, stream, "asrattn_fwd_fsmn");
 }
 
 int asrattn_decode_num_splits(const asrattn_decode_params* params) {

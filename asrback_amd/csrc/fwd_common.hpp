@@ -2,12 +2,14 @@
 #pragma once
 
 #include "common.hpp"
+#include "fsmn.hpp"
 
 namespace asrattn {
 
 struct FwdArgs {
   asrattn_fwd_params p;
   float c;  // scale * log2(e)
+  FsmnArgs f;  // the fused FSMN memory (f.memory null: none)
 };
 
 // Resolved geometry of one (sequence, head): element offsets of its first

@@ -42,6 +42,13 @@
 // Work mapping: a flat grid of (sequence, head, query tile) items, taken
 // longest-first in ragged batches, with the query tiles of one (sequence,
 // head) -- and its K/V -- on one XCD's L2 (work_item).
+//
+// SAN-M's FSMN memory (fsmn.hpp) can ride along: the grid then holds a
+// second copy of the items, each computing the memory of its row block.
+// Dispatched after every attention item, they take the CUs that short
+// sequences free while the longest ones finish; computed instead at the end
+// of each attention item, the memory lengthened the longest items (and, with
+// the tap-pair code, spilled).
 #include "common.hpp"
 #include "fwd_common.hpp"
 #include "kernels.hpp"
@@ -153,9 +160,8 @@ __device__ __forceinline__ int ranked_sequence(const asrattn_fwd_params& p, int 
 // XCD P % 8 with its query tiles consecutive there, so its K/V stay in one
 // L2.  Otherwise ids are remapped so that each XCD gets a contiguous range of
 // items (the same L2 grouping).
-__device__ __forceinline__ void work_item(const asrattn_fwd_params& p, int q_tiles, int total, int& b, int& hq,
-                                          int& qt) {
-  const int id = blockIdx.x;
+__device__ __forceinline__ void work_item(const asrattn_fwd_params& p, int q_tiles, int total, int id, int& b,
+                                          int& hq, int& qt) {
   const bool ragged = p.seqused_k != nullptr || p.cu_seqlens_k != nullptr;
   if (ragged && p.batch <= 64 && (p.batch * p.heads_q) % 8 == 0) {
     const int k = id >> 3;
@@ -217,7 +223,7 @@ __device__ __forceinline__ int v_phys(int r, int c) {
   return HD == 128 ? (c ^ (4 * (r & 3))) : (c ^ (4 * ((r >> 1) & 1)));
 }
 
-template <int HD, int RB, int KS, int BN, int ST, int OCC>
+template <int HD, int RB, int KS, int BN, int ST, int OCC, int FS>
 __global__ __launch_bounds__(64 * RB * KS, OCC) void fwd_ring_kernel(const FwdArgs a, int q_tiles, int total) {
   using S = RingShape<HD, RB, KS, BN, ST>;
   constexpr int BM = S::kBM, KST = S::kKSteps, DB = S::kDB, KB = S::kKB, RBYTES = S::kRowBytes;
@@ -225,14 +231,34 @@ __global__ __launch_bounds__(64 * RB * KS, OCC) void fwd_ring_kernel(const FwdAr
   constexpr int SPAN = S::kSpan;
   const asrattn_fwd_params& p = a.p;
 
+  const int tid = threadIdx.x;
+  __shared__ __attribute__((aligned(16))) unsigned char lds[S::kLds];
+
+  // FSMN items (ids total .. 2 total - 1, same (sequence, head, row block)
+  // and XCD as attention item id - total): the memory of the block's rows.
+  // They are dispatched after every attention item and fill the CUs that
+  // short sequences leave idle while the longest ones finish.
+  if constexpr (FS > 0) {
+    if ((int)blockIdx.x >= total) {
+      int b, h, qt;
+      work_item(p, q_tiles, total, (int)blockIdx.x - total, b, h, qt);
+      const SeqView sv = seq_view(p, b, h, h);
+      constexpr int NT = S::kThreads;
+      static_assert(fsmn_lds_bytes<bf16_raw, HD, FS>() <= S::kLds, "FSMN filter fits the LDS");
+      fsmn_rows<bf16_raw, HD, FS, BM * (HD / 4) / NT, NT>(a.f, static_cast<const bf16_raw*>(p.v) + sv.v_off,
+                                                         p.v_token_stride, b, h, qt * BM, sv.n_k, sv.len_q, tid,
+                                                         lds);
+      return;
+    }
+  }
+
   int b, hq, qt;
-  work_item(p, q_tiles, total, b, hq, qt);
+  work_item(p, q_tiles, total, (int)blockIdx.x, b, hq, qt);
   const int hkv = hq / (p.heads_q / p.heads_kv);
   const SeqView sv = seq_view(p, b, hq, hkv);
   const int row0 = qt * BM;
   if (row0 >= sv.len_q) return;  // uniform over the workgroup
 
-  const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: DMA destinations live in SGPRs
   const int rb = wave % RB;  // row block
@@ -248,7 +274,6 @@ __global__ __launch_bounds__(64 * RB * KS, OCC) void fwd_ring_kernel(const FwdAr
   const int wkend = wrow0 < sv.len_q ? visible_keys(p, sv, min(wrow0 + 32, sv.len_q) - 1) : 0;
   const int n_tiles = (kend + SPAN - 1) / SPAN;
 
-  __shared__ __attribute__((aligned(16))) unsigned char lds[S::kLds];
   // Low 32 bits of the flat address of an LDS variable are its LDS offset.
   const uint32_t lds_base = (uint32_t)(uintptr_t)lds;
 
@@ -450,6 +475,7 @@ __global__ __launch_bounds__(64 * RB * KS, OCC) void fwd_ring_kernel(const FwdAr
   }
   __syncthreads();  // the ring is free for the merge and the output staging
 
+
   // Merge the key splits of each row block through LDS; afterwards wave
   // (rb, 0) stages its rows in the first merge slot of its row block (which
   // only it reads) or, without splits, in its own region.
@@ -524,15 +550,18 @@ __global__ __launch_bounds__(64 * RB * KS, OCC) void fwd_ring_kernel(const FwdAr
   }
 }
 
-template <int HD, int RB, int KS, int BN, int ST, int OCC>
+template <int HD, int RB, int KS, int BN, int ST, int OCC, int FS>
 hipError_t launch_typed(const FwdArgs& a, hipStream_t stream) {
   using S = RingShape<HD, RB, KS, BN, ST>;
   const asrattn_fwd_params& p = a.p;
   const int q_tiles = (p.max_len_q + S::kBM - 1) / S::kBM;
   const long long total = (long long)q_tiles * p.heads_q * p.batch;
   if (total <= 0) return hipSuccess;
-  if (total > 0x7fffffffLL) return hipErrorInvalidConfiguration;
-  hipLaunchKernelGGL((fwd_ring_kernel<HD, RB, KS, BN, ST, OCC>), dim3((unsigned)total), dim3(S::kThreads), 0, stream, a,
+  // With FSMN items the grid holds every item twice (attention, then FSMN).
+  const int copies = FS > 0 ? 2 : 1;
+  if (copies * total > 0x7fffffffLL) return hipErrorInvalidConfiguration;
+  const unsigned grid = (unsigned)(copies * total);
+  hipLaunchKernelGGL((fwd_ring_kernel<HD, RB, KS, BN, ST, OCC, FS>), dim3(grid), dim3(S::kThreads), 0, stream, a,
                      q_tiles, (int)total);
   return hipGetLastError();
 }
@@ -543,7 +572,8 @@ hipError_t launch_hd(const FwdArgs& a, hipStream_t stream) {
   // two workgroups per CU, whose waves pair up on the SIMDs without sharing
   // a barrier.  Key splits (KS > 1) halve the rows a CU holds at two waves
   // per SIMD, which costs more than they save once the batch fills the GPU.
-  return launch_typed<HD, 4, 1, 64, 2, 2>(a, stream);
+  if (a.f.memory != nullptr) return launch_typed<HD, 4, 1, 64, 2, 2, kFsmnFusedKernel>(a, stream);
+  return launch_typed<HD, 4, 1, 64, 2, 2, 0>(a, stream);
 }
 
 }  // namespace
@@ -560,10 +590,11 @@ bool fwd_ring_supported(const asrattn_fwd_params& p) {
   return span_k < (1LL << 31) && span_v < (1LL << 31);
 }
 
-hipError_t launch_fwd_ring(const asrattn_fwd_params& p, hipStream_t stream) {
+hipError_t launch_fwd_ring(const asrattn_fwd_params& p, const FsmnArgs* fsmn, hipStream_t stream) {
   FwdArgs a;
   a.p = p;
   a.c = p.scale * kLog2e;
+  a.f = fsmn != nullptr ? *fsmn : FsmnArgs{};
   return p.head_dim == 64 ? launch_hd<64>(a, stream) : launch_hd<128>(a, stream);
 }
 

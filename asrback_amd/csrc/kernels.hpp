@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 
 #include "asrattn.h"
+#include "fsmn.hpp"
 
 namespace asrattn {
 
@@ -20,7 +21,9 @@ bool decode_supported(int dtype, int head_dim, int group);
 
 // Multi-row forward on matrix cores with K/V streamed into an LDS ring by
 // DMA (bf16, head_dim 64 or 128, K/V spans addressable with 32-bit offsets).
-hipError_t launch_fwd_ring(const asrattn_fwd_params& p, hipStream_t stream);
+// fsmn (or null): the FSMN memory computed in the same launch (kernel size
+// at most kFsmnFusedKernel).
+hipError_t launch_fwd_ring(const asrattn_fwd_params& p, const FsmnArgs* fsmn, hipStream_t stream);
 bool fwd_ring_supported(const asrattn_fwd_params& p);
 
 // Greedy choice per row of fp32 logits: argmax (first index on ties) and its
@@ -33,5 +36,10 @@ hipError_t launch_choose(const float* logits, int64_t rows, int64_t vocab, int64
 // not address, and the reference-precision check of that kernel.
 hipError_t launch_fwd_valu(const asrattn_fwd_params& p, hipStream_t stream);
 bool fwd_valu_supported(int dtype, int head_dim);
+
+// SAN-M's FSMN memory on its own (fp32 or bf16, head_dim 64 or 128, kernel
+// size at most kFsmnMaxKernel) for the padded layout of p (values p.v, frame
+// counts p.seqused_k).
+hipError_t launch_fsmn(const asrattn_fwd_params& p, const FsmnArgs& f, hipStream_t stream);
 
 }  // namespace asrattn

@@ -3,11 +3,14 @@
 Drop-in for the network classes of the reference's ``models/sensevoice.py``
 (``:66-212``): same class names, parameter names (FunASR checkpoint names)
 and ``forward(x, mask, lengths)`` signatures.  ``SANMAttention`` runs its
-attention on :func:`asrback_amd.attention.flash` directly over views of the
-fused ``linear_q_k_v`` output (token stride ``3 * size``), with the padding
+attention and its FSMN memory in one kernel call
+(:func:`asrback_amd.attention.flash_fsmn`) directly over views of the fused
+``linear_q_k_v`` output (token stride ``3 * size``), with the padding
 expressed as ``seqused_k = lengths``: the reference's ``varlen_attn`` path
-(``sensevoice.py:110-125``) and its masked-SDPA fallback (``:126-133``)
-become one kernel call in every dtype.  The FSMN memory stays in PyTorch.
+(``sensevoice.py:110-125``), its masked-SDPA fallback (``:126-133``) and the
+masked depthwise convolution (``:99-107``) become one launch, and
+``linear_out(attention) + memory`` one GEMM accumulating into the memory
+(which carries ``linear_out``'s bias).
 """
 
 from __future__ import annotations
@@ -18,7 +21,7 @@ import torch
 import torch.nn.functional as F
 from torch import Tensor, nn
 
-from .attention import flash
+from .attention import flash_fsmn
 
 
 class SANMAttention(nn.Module):
@@ -32,29 +35,31 @@ class SANMAttention(nn.Module):
         self.linear_q_k_v = nn.Linear(in_size, size * 3)
         self.linear_out = nn.Linear(size, size)
         self.fsmn_block = nn.Conv1d(size, size, kernel_size, padding=0, groups=size, bias=False)
-        left = (kernel_size - 1) // 2
-        self.padding = (left, kernel_size - 1 - left)
+        if not 1 <= kernel_size <= 15:
+            raise ValueError(f"FSMN kernel_size {kernel_size} is outside the supported 1..15")
 
     def forward(self, x: Tensor, mask: Tensor | None, lengths: Tensor | None) -> Tensor:
-        """``mask`` is ``(batch, length)``, True for real frames, and
-        ``lengths`` (int32) counts them per row; both are None when every
-        frame is real."""
+        """``mask`` is ``(batch, length)``, True for the first ``lengths[b]``
+        frames of row b (the frame mask ``sensevoice.py:548-550`` builds), and
+        ``lengths`` (int32) counts them; both are None when every frame is
+        real."""
         qkv = self.linear_q_k_v(x)
         query, key, value = qkv.split(self.size, dim=-1)
-
-        keep = None if mask is None else mask[..., None].to(value.dtype)
-        value_masked = value if keep is None else value * keep
-        memory = F.pad(value_masked.transpose(1, 2), self.padding)
-        memory = self.fsmn_block(memory).transpose(1, 2) + value_masked
-        if keep is not None:
-            memory = memory * keep
-
         batch, length, _ = x.shape
         if lengths is None and mask is not None:
             lengths = mask.sum(dim=1, dtype=torch.int32)
         shape = (batch, length, self.heads, self.size // self.heads)
-        output = flash(query.view(shape), key.view(shape), value.view(shape), seqused_k=lengths)
-        return self.linear_out(output.reshape(batch, length, self.size)) + memory
+        output, memory = flash_fsmn(
+            query.view(shape),
+            key.view(shape),
+            value.view(shape),
+            self.fsmn_block.weight,
+            seqused_k=lengths,
+            bias=self.linear_out.bias,
+        )
+        # linear_out(output) + memory: the bias is in memory already.
+        memory.view(-1, self.size).addmm_(output.view(-1, self.size), self.linear_out.weight.t())
+        return memory
 
 
 class FeedForward(nn.Module):

@@ -17,9 +17,10 @@ a (28, 64, 1024, 8, 128) cache, 128 steps) and Whisper-small's decoder step
 plus q and o), and the Qwen3 step with its prologue (per-head RMSNorm and
 rotary embedding of q and k, the cache write) fused into the decode launch,
 timed beside the unfused sequence of ops, and the greedy token choice over
-Qwen3's (64, 151936) logits in one pass.  ``secondary`` adds Whisper
-large-v3-turbo's encoder attention
-(20 heads x 64, 1500 frames, batch 16, 32 layers).
+Qwen3's (64, 151936) logits in one pass.  ``secondary`` adds the SenseVoice
+attention with its FSMN memory fused into the same launch (timed beside the
+reference's ops for both outputs) and Whisper large-v3-turbo's encoder
+attention (20 heads x 64, 1500 frames, batch 16, 32 layers).
 
 ``cpu_baseline`` times the CPU restatement of the reference's attention
 (torch SDPA with the key-padding mask, float32, the reference's CPU path) on
@@ -117,6 +118,60 @@ class SenseVoiceEncoder(Workload):
             "lengths_mean": float(self.lengths_host.mean()),
             "max_length": self.length,
         }
+
+
+class SenseVoiceAttentionFsmn(SenseVoiceEncoder):
+    """The SAN-M attention and its FSMN memory (sensevoice.py:97-135) on the
+    headline batch, one ``flash_fsmn`` launch per layer (kernel 11).  Value:
+    attention FLOPs per second as for the attention alone.
+    ``unfused_ms_per_step`` times the reference's ops for the same two
+    outputs (mask multiply, pad, depthwise conv1d, add, mask multiply, then
+    the attention kernel); ``module_ms_per_step`` / ``module_unfused_ms_per_step``
+    add ``linear_out(attention) + memory`` (one GEMM accumulating into the
+    memory, against linear and add)."""
+
+    name = "sensevoice-small-attention-fsmn"
+
+    def __init__(self, torch, attention, seed: int = 1) -> None:
+        super().__init__(torch, attention, seed)
+        g = torch.Generator(device="cuda").manual_seed(seed + 7)
+        width = self.heads * self.head_dim
+        self.weight = [(torch.randn((width, 1, 11), generator=g, device="cuda") * 0.3).to(torch.bfloat16)
+                       for _ in range(self.layers)]
+        self.bias = [torch.randn(width, generator=g, device="cuda").to(torch.bfloat16) for _ in range(self.layers)]
+        self.w_out = [(torch.randn((width, width), generator=g, device="cuda") / width ** 0.5).to(torch.bfloat16)
+                      for _ in range(self.layers)]
+        frames = torch.arange(self.length, device="cuda")[None, :] < self.lengths[:, None].long()
+        self.keep = frames[..., None].to(torch.bfloat16)
+        self.memory = torch.empty((self.batch, self.length, width), device="cuda", dtype=torch.bfloat16)
+        self.torch = torch
+        self.mode = "fused"
+
+    def run(self) -> None:
+        F = self.torch.nn.functional
+        width = self.heads * self.head_dim
+        module = self.mode.startswith("module")
+        for layer in range(self.layers):
+            q, k, v = self.views(layer)
+            if self.mode in ("fused", "module"):
+                self.attention.flash_fsmn(q, k, v, self.weight[layer], seqused_k=self.lengths,
+                                          bias=self.bias[layer] if module else None, out=self.out,
+                                          memory=self.memory)
+                if module:
+                    self.memory.view(-1, width).addmm_(self.out.view(-1, width), self.w_out[layer].t())
+                continue
+            masked = self.qkv[layer][..., 2 * width:] * self.keep
+            memory = F.pad(masked.transpose(1, 2), (5, 5))
+            memory = F.conv1d(memory, self.weight[layer], groups=width).transpose(1, 2) + masked
+            memory = memory * self.keep
+            self.attention.flash(q, k, v, seqused_k=self.lengths, out=self.out)
+            if module:
+                memory = F.linear(self.out.view(self.batch, self.length, width), self.w_out[layer],
+                                  self.bias[layer]) + memory
+            self.memory.copy_(memory)
+
+    def config(self) -> dict:
+        return {**super().config(), "workload": self.name, "fsmn_kernel": 11}
 
 
 class WhisperTurboEncoder(Workload):
@@ -473,6 +528,17 @@ def measure(torch, workload: Workload, steps: int, warmup: int) -> dict:
         workload.unfused = False
         result["unfused_ms_per_step"] = round(unfused, 4)
         result["speedup_vs_unfused"] = round(unfused / ms, 3)
+    if isinstance(workload, SenseVoiceAttentionFsmn):
+        timed = {}
+        for mode in ("unfused", "module", "module_unfused"):
+            workload.mode = mode
+            timed[mode] = time_graph(torch, workload, steps, warmup)
+        workload.mode = "fused"
+        result["unfused_ms_per_step"] = round(timed["unfused"], 4)
+        result["speedup_vs_unfused"] = round(timed["unfused"] / ms, 3)
+        result["module_ms_per_step"] = round(timed["module"], 4)
+        result["module_unfused_ms_per_step"] = round(timed["module_unfused"], 4)
+        result["module_speedup_vs_unfused"] = round(timed["module_unfused"] / timed["module"], 3)
     if isinstance(workload, Qwen3DecodeStepFused):
         workload.unfused = True
         unfused = time_graph(torch, workload, steps, min(warmup, workload.steps), reset=workload.reset)
@@ -582,8 +648,8 @@ def main() -> int:
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--no-cpu-baseline", action="store_true")
-    parser.add_argument("--only", choices=["sensevoice", "turbo", "qwen3", "qwen3-fused", "whisper-small", "choice",
-                                           "copy"],
+    parser.add_argument("--only", choices=["sensevoice", "sensevoice-fsmn", "turbo", "qwen3", "qwen3-fused",
+                                           "whisper-small", "choice", "copy"],
                         default=None,
                         help="measure one workload only (for profiling)")
     parser.add_argument("--sweep", action="store_true",
@@ -611,6 +677,7 @@ def main() -> int:
         return 0
     selected = {
         "sensevoice": SenseVoiceEncoder,
+        "sensevoice-fsmn": SenseVoiceAttentionFsmn,
         "turbo": WhisperTurboEncoder,
         "qwen3": Qwen3Decode,
         "qwen3-fused": Qwen3DecodeStepFused,
@@ -633,9 +700,11 @@ def main() -> int:
         log(f"bench: {cls.name}")
         decode.append(measure(torch, cls(torch, attention), args.steps, args.warmup))
         torch.cuda.empty_cache()
-    log("bench: whisper turbo encoder attention")
-    secondary = [measure(torch, WhisperTurboEncoder(torch, attention), args.steps, args.warmup)]
-    torch.cuda.empty_cache()
+    secondary = []
+    for cls in (SenseVoiceAttentionFsmn, WhisperTurboEncoder):
+        log(f"bench: {cls.name}")
+        secondary.append(measure(torch, cls(torch, attention), args.steps, args.warmup))
+        torch.cuda.empty_cache()
     baseline = None
     if not args.no_cpu_baseline:
         log("bench: cpu baseline")

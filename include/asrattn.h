@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define ASRATTN_ABI_VERSION 2
+#define ASRATTN_ABI_VERSION 3
 
 enum asrattn_status {
   ASRATTN_OK = 0,
@@ -109,6 +109,39 @@ typedef struct asrattn_fwd_params {
 } asrattn_fwd_params;
 
 int asrattn_fwd(const asrattn_fwd_params* params, void* stream);
+
+/*
+ * SAN-M self-attention with its FSMN memory, in one launch where the
+ * matrix-core kernel applies (bf16, kernel_size <= 11): asrattn_fwd on the
+ * padded, non-causal layout (cu_seqlens NULL, heads_q == heads_kv,
+ * max_len_q == max_len_k; seqused_k, the frame counts n_b, or NULL for all
+ * frames) and, over the values v of the same call,
+ *
+ *   memory[b, t, c] = keep(t) * (conv + v'[b, t, c]) + bias[c]     (t < max_len_q)
+ *   conv            = sum_{i < K} weight[c, i] * v'[b, t + i - (K - 1) / 2, c]
+ *   v'[b, s, c]     = v[b, s, h, d] if 0 <= s < n_b else 0,  keep(t) = t < n_b
+ *
+ * with channel c = h * head_dim + d.  Rounded in the element type as the
+ * reference's ops round: the convolution (fp32 sums), then the sum with v',
+ * then the sum with the bias.  bias (or NULL) lets the caller fold the
+ * output projection's bias in: linear_out(out) + memory becomes one GEMM
+ * that accumulates into memory.  memory must not overlap q, k, v or out.
+ *
+ * Replaces (the reference's mask multiply, pad, depthwise Conv1d, add, mask
+ * multiply and the final add):
+ *   sensevoice.py:99-107 (FSMN memory) and :135 (linear_out(...) + memory)
+ *                                    src/asrback/models/sensevoice.py
+ * together with the attention call of asrattn_fwd (sensevoice.py:110-133).
+ */
+typedef struct asrattn_fsmn_params {
+  const void* weight; /* (heads_q * head_dim, kernel_size): Conv1d weight (C, 1, K), contiguous */
+  const void* bias;   /* (heads_q * head_dim) added to every row, or NULL */
+  void* memory;       /* (batch, max_len_q, heads_q * head_dim), unit channel stride */
+  int64_t m_batch_stride, m_token_stride;
+  int32_t kernel_size; /* 1 .. 15 */
+} asrattn_fsmn_params;
+
+int asrattn_fwd_fsmn(const asrattn_fwd_params* params, const asrattn_fsmn_params* fsmn, void* stream);
 
 /*
  * One query per sequence over a key/value cache (decoder step).  A

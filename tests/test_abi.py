@@ -38,6 +38,7 @@ def lib():
 def test_header_declares_expected_entry_points():
     assert declared_functions() == {
         "asrattn_fwd",
+        "asrattn_fwd_fsmn",
         "asrattn_decode",
         "asrattn_decode_append",
         "asrattn_choose",
@@ -85,13 +86,13 @@ def _c_layout(struct: str, fields: list[str]) -> dict[str, int]:
     return {k: int(v) for k, v in (line.split() for line in out.splitlines())}
 
 
-@pytest.mark.parametrize("name", ["FwdParams", "DecodeParams", "AppendParams"])
+@pytest.mark.parametrize("name", ["FwdParams", "DecodeParams", "AppendParams", "FsmnParams"])
 def test_ctypes_structs_match_c_layout(name):
     from asrback_amd import _lib
 
     cls = getattr(_lib, name)
     struct = {"FwdParams": "asrattn_fwd_params", "DecodeParams": "asrattn_decode_params",
-              "AppendParams": "asrattn_append_params"}[name]
+              "AppendParams": "asrattn_append_params", "FsmnParams": "asrattn_fsmn_params"}[name]
     fields = [f for f, _ in cls._fields_]
     layout = _c_layout(struct, fields)
     assert layout.pop("sizeof") == ctypes.sizeof(cls)
@@ -162,6 +163,46 @@ def test_invalid_append_and_span_are_reported(lib):
     p.positions, p.max_len_k = 0, 1 << 23
     assert lib.asrattn_decode(ctypes.byref(p), None, 0, None) == _lib.ERR_UNSUPPORTED
     assert b"2 GiB" in lib.asrattn_last_error()
+
+
+def test_invalid_fsmn_arguments_are_reported(lib):
+    """asrattn_fwd_fsmn's own checks, before any device call (stand-in
+    pointers, never dereferenced)."""
+    from asrback_amd import _lib
+
+    f = _lib.FwdParams()
+    f.batch, f.heads_q, f.heads_kv, f.head_dim = 2, 4, 4, 128
+    f.max_len_q = f.max_len_k = 40
+    f.dtype, f.scale = _lib.BF16, 0.125
+    f.q, f.k, f.v, f.out = 4096, 4096 + 1024, 4096 + 2048, 1 << 20
+    for prefix in ("q", "k", "v"):
+        setattr(f, f"{prefix}_batch_stride", 40 * 1536)
+        setattr(f, f"{prefix}_token_stride", 1536)
+        setattr(f, f"{prefix}_head_stride", 128)
+    f.o_batch_stride, f.o_token_stride, f.o_head_stride = 40 * 512, 512, 128
+    m = _lib.FsmnParams()
+    assert lib.asrattn_fwd_fsmn(ctypes.byref(f), None, None) == _lib.ERR_INVALID
+    assert lib.asrattn_fwd_fsmn(ctypes.byref(f), ctypes.byref(m), None) == _lib.ERR_UNSUPPORTED
+    assert b"kernel_size" in lib.asrattn_last_error()
+    m.kernel_size = 11
+    assert lib.asrattn_fwd_fsmn(ctypes.byref(f), ctypes.byref(m), None) == _lib.ERR_INVALID
+    assert b"non-NULL" in lib.asrattn_last_error()
+    m.weight, m.memory, m.m_batch_stride, m.m_token_stride = 8192, 4100, 40 * 512, 512  # memory misaligned
+    assert lib.asrattn_fwd_fsmn(ctypes.byref(f), ctypes.byref(m), None) == _lib.ERR_INVALID
+    assert b"16-byte" in lib.asrattn_last_error()
+    m.memory = 1 << 24
+    f.causal = _lib.CAUSAL_TOP_LEFT
+    assert lib.asrattn_fwd_fsmn(ctypes.byref(f), ctypes.byref(m), None) == _lib.ERR_INVALID
+    assert b"non-causal" in lib.asrattn_last_error()
+    f.causal, f.heads_kv = _lib.CAUSAL_NONE, 2
+    assert lib.asrattn_fwd_fsmn(ctypes.byref(f), ctypes.byref(m), None) == _lib.ERR_INVALID
+    f.heads_kv, f.max_len_k = 4, 39
+    assert lib.asrattn_fwd_fsmn(ctypes.byref(f), ctypes.byref(m), None) == _lib.ERR_INVALID
+    f.max_len_k, m.kernel_size = 40, 16
+    assert lib.asrattn_fwd_fsmn(ctypes.byref(f), ctypes.byref(m), None) == _lib.ERR_UNSUPPORTED
+    # Nothing to do: no device call, no error.
+    m.kernel_size, f.batch = 11, 0
+    assert lib.asrattn_fwd_fsmn(ctypes.byref(f), ctypes.byref(m), None) == _lib.OK
 
 
 def test_workspace_size_and_split_choice(lib):

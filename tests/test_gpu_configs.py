@@ -65,6 +65,96 @@ def test_sensevoice_unmasked_equals_masked_full_length(ops, device):
     assert torch.equal(full, masked)
 
 
+def _fsmn_reference(fused, heads, lengths, weight, bias):
+    """The oracle's FSMN memory (sensevoice.py:99-107) in float32 on the
+    values of ``fused``, plus ``bias`` on every row."""
+    size = fused.shape[-1] // 3
+    mask = None if lengths is None else oa.key_padding_mask(lengths, fused.shape[1])
+    memory = oa.fsmn_memory(fused[..., 2 * size :].float(), mask, weight.float(), weight.shape[-1])
+    return memory if bias is None else memory + bias.float()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_sensevoice_fsmn_fused_matches_oracle(ops, device, dtype):
+    """Attention plus FSMN memory in one call at the SenseVoice batch shape
+    (B=32, 4 x 128, lengths 4 + U{100..500}, kernel 11, linear_out's bias
+    folded in): the attention output equals asrattn_fwd's, the memory
+    matches the oracle's masked depthwise convolution, and padded rows hold
+    the bias alone."""
+    say("sensevoice fsmn fused", dtype)
+    rng = np.random.default_rng(13)
+    lengths = torch.from_numpy((rng.integers(100, 501, size=32) + 4).astype(np.int32))
+    length = int(lengths.max())
+    fused = randn(32, length, 1536, seed=13, dtype=dtype)
+    weight = (randn(512, 1, 11, seed=14) * 0.3).to(dtype)
+    bias = randn(512, seed=15, dtype=dtype)
+    x = fused.to(device)
+    q, k, v = (t.view(32, length, 4, 128) for t in x.split(512, dim=-1))
+    used = lengths.to(device)
+    out, memory = ops.flash_fsmn(q, k, v, weight.to(device), seqused_k=used, bias=bias.to(device))
+    assert torch.equal(out, ops.flash(q, k, v, seqused_k=used))
+    ref = _fsmn_reference(fused, 4, lengths, weight, bias)
+    assert max_rel_err(memory.cpu(), ref) < TOL[dtype]
+    for b in (int(lengths.argmin()), 0):
+        n = int(lengths[b])
+        assert torch.equal(memory[b, n:].cpu(), bias.expand(length - n, 512))
+
+
+@pytest.mark.parametrize(
+    "dtype,heads,head_dim,kernel,force_valu",
+    [
+        (torch.bfloat16, 4, 128, 11, False),
+        (torch.bfloat16, 4, 128, 5, False),
+        (torch.bfloat16, 4, 128, 4, False),
+        (torch.bfloat16, 4, 128, 15, False),
+        (torch.bfloat16, 8, 64, 11, False),
+        (torch.bfloat16, 4, 128, 11, True),
+        (torch.float32, 4, 128, 11, False),
+        (torch.float32, 2, 64, 10, False),
+        (torch.float32, 4, 128, 1, False),
+        (torch.float32, 2, 64, 15, False),
+    ],
+)
+def test_fsmn_kernel_sizes_and_edges(ops, device, dtype, heads, head_dim, kernel, force_valu):
+    """Filter sizes 1..15 (odd and even: left padding (K - 1) // 2), both
+    head sizes, the fused epilogue and the separate kernel; rows of 0, 2
+    and 37 frames (shorter than the filter's reach) and one full row of 130
+    (two row blocks, the second of two rows)."""
+    say("fsmn", dtype, heads, head_dim, kernel, force_valu)
+    lengths = torch.tensor([37, 130, 2, 0], dtype=torch.int32)
+    width = heads * head_dim
+    fused = randn(4, 130, 3 * width, seed=16, dtype=dtype)
+    weight = (randn(width, 1, kernel, seed=17) * 0.3).to(dtype)
+    x = fused.to(device)
+    q, k, v = (t.view(4, 130, heads, head_dim) for t in x.split(width, dim=-1))
+    out, memory = ops.flash_fsmn(
+        q, k, v, weight.to(device), seqused_k=lengths.to(device), force_valu=force_valu
+    )
+    ref = _fsmn_reference(fused, heads, lengths, weight, None)
+    assert max_rel_err(memory.cpu(), ref) < TOL[dtype]
+    assert not memory[3].any() and not memory[2, 2:].any()
+    # (the frame-less row's reference is NaN: softmax over no keys)
+    valid = oa.key_padding_mask(lengths, 130)
+    attention = oa.sensevoice_attention(fused.float(), heads, valid)
+    assert max_rel_err(out.reshape(4, 130, width).cpu()[valid], attention[valid]) < TOL[dtype]
+    # Without frame counts every frame is real.
+    _, full = ops.flash_fsmn(q, k, v, weight.to(device), force_valu=force_valu)
+    assert max_rel_err(full.cpu(), _fsmn_reference(fused, heads, None, weight, None)) < TOL[dtype]
+
+
+def test_fsmn_fused_epilogue_equals_separate_kernel(ops, device):
+    """The attention kernel's FSMN epilogue and the FSMN kernel of its own
+    compute the same sums in the same order: identical bits."""
+    lengths = torch.tensor([300, 17, 256, 129], dtype=torch.int32, device=device)
+    x = randn(4, 300, 1536, seed=18, dtype=torch.bfloat16).to(device)
+    weight = (randn(512, 1, 11, seed=19) * 0.3).to(torch.bfloat16).to(device)
+    bias = randn(512, seed=20, dtype=torch.bfloat16).to(device)
+    q, k, v = (t.view(4, 300, 4, 128) for t in x.split(512, dim=-1))
+    _, fused = ops.flash_fsmn(q, k, v, weight, seqused_k=lengths, bias=bias)
+    _, separate = ops.flash_fsmn(q, k, v, weight, seqused_k=lengths, bias=bias, force_valu=True)
+    assert torch.equal(fused, separate)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_whisper_encoder_shapes(ops, device, dtype):
     """Whisper encoder self-attention over 1500 frames: large-v3-turbo's 20

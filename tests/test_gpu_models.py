@@ -92,6 +92,30 @@ def test_sensevoice_padding_invariance(device):
             assert max_rel_err(batched[b, : 4 + n].cpu(), alone[0].cpu()) < 1e-5
 
 
+def test_sensevoice_layer_bf16_matches_oracle(device):
+    """One SAN-M attention module in bfloat16 (fused attention + FSMN, one
+    GEMM for linear_out + memory) against the oracle's module in float32 on
+    the same bf16-rounded weights and inputs; padded rows are compared too
+    (they carry linear_out's bias plus the projection of their attention)."""
+    from asrback_amd import sensevoice as asv
+
+    say("sensevoice layer bf16")
+    ref = osv.SANMAttention(512, 512, 4, 11).eval()
+    state = {k: v.to(torch.bfloat16).float() for k, v in named_weights(ref, 8).items()}
+    ref.load_state_dict(state)
+    model = asv.SANMAttention(512, 512, 4, 11)
+    model.load_state_dict(state, strict=True)
+    model = model.eval().to(device=device, dtype=torch.bfloat16)
+    frames = torch.tensor([300, 120, 9, 257])
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(4, 300, 512, generator=g).to(torch.bfloat16)
+    mask = osv.frame_mask(frames, 0, 300)
+    with torch.inference_mode():
+        expected = ref(x.float(), mask, None)
+        out = model(x.to(device), mask.to(device), None)
+    assert max_rel_err(out.float().cpu(), expected) < 2e-2
+
+
 # --- Qwen3-ASR -------------------------------------------------------------------
 
 
