@@ -19,7 +19,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must be imported before the library; see above)
 
 LIBRARY = Path(__file__).resolve().with_name("libasrattn.so")
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 # enum asrattn_status / asrattn_dtype / asrattn_causal
 OK = 0
@@ -138,6 +138,19 @@ class FsmnParams(ctypes.Structure):
     ]
 
 
+class PagedKV(ctypes.Structure):
+    """``asrattn_paged_kv``."""
+
+    _fields_ = [
+        ("block_table", _ptr),
+        ("bt_stride", _i64),
+        ("page_size", _i32),
+        ("num_pages", _i32),
+        ("k_page_stride", _i64),
+        ("v_page_stride", _i64),
+    ]
+
+
 # Every symbol include/asrattn.h declares, with (restype, argtypes).
 SIGNATURES = {
     "asrattn_fwd": (ctypes.c_int, [ctypes.POINTER(FwdParams), _ptr]),
@@ -149,6 +162,11 @@ SIGNATURES = {
     "asrattn_decode_append": (
         ctypes.c_int,
         [ctypes.POINTER(DecodeParams), ctypes.POINTER(AppendParams), _ptr, ctypes.c_size_t, _ptr],
+    ),
+    "asrattn_decode_paged": (
+        ctypes.c_int,
+        [ctypes.POINTER(DecodeParams), ctypes.POINTER(AppendParams), ctypes.POINTER(PagedKV), _ptr,
+         ctypes.c_size_t, _ptr],
     ),
     "asrattn_choose": (
         ctypes.c_int,

@@ -75,6 +75,46 @@ class KeyPrefix:
         return cls(lengths=lengths)
 
 
+@dataclass(frozen=True)
+class PageTable:
+    """A paged key/value layout for :func:`decode` / :func:`decode_append`:
+    the cache tensors are pools ``(num_pages, page_size, heads_kv,
+    head_dim)`` and logical page ``i`` of sequence ``b`` (its keys ``i *
+    page_size ..``) is pool page ``block_table[b, i]`` (int32 ``(batch,
+    pages_per_row)``, on the device; entries outside the pool are skipped).
+    ``max_len`` bounds the keys a sequence may use (default: the table's
+    reach).  Generalizes the reference's fixed ``row * 1024`` slab
+    (``qwen3_asr.py:511-512``)."""
+
+    block_table: Tensor
+    max_len: int | None = None
+
+    def __post_init__(self) -> None:
+        if self.block_table.dtype != torch.int32 or self.block_table.dim() != 2:
+            raise TypeError("block_table must be an int32 (batch, pages_per_row) tensor")
+        if self.block_table.stride(-1) != 1:
+            raise ValueError("block_table rows must be contiguous")
+
+
+def _paged(pages: PageTable, k: Tensor, v: Tensor, batch: int) -> tuple[_lib.PagedKV, int]:
+    """``asrattn_paged_kv`` for pools ``k``/``v`` and the keys a sequence may use."""
+    table = pages.block_table
+    if table.shape[0] < batch:
+        raise ValueError(f"block_table has {table.shape[0]} rows for {batch} sequences")
+    page_size = k.shape[1]
+    reach = table.shape[1] * page_size
+    max_len = reach if pages.max_len is None else pages.max_len
+    if not 0 <= max_len <= reach:
+        raise ValueError(f"max_len {max_len} outside the table's reach {reach}")
+    pk = _lib.PagedKV()
+    pk.block_table = table.data_ptr()
+    pk.bt_stride = table.stride(0)
+    pk.page_size = page_size
+    pk.num_pages = k.shape[0]
+    pk.k_page_stride, pk.v_page_stride = k.stride(0), v.stride(0)
+    return pk, max_len
+
+
 def _dtype_code(*tensors: Tensor) -> int:
     dtype = tensors[0].dtype
     if dtype not in _DTYPES:
@@ -347,13 +387,16 @@ def decode(
     scale: float | None = None,
     out: Tensor | None = None,
     workspace: Tensor | None = None,
+    pages: PageTable | None = None,
 ) -> Tensor:
-    """One query per sequence over a cache (``asrattn_decode``).
+    """One query per sequence over a cache (``asrattn_decode``, or
+    ``asrattn_decode_paged`` with ``pages``).
 
     ``q`` ``(batch, heads_q, head_dim)``; ``k``/``v`` ``(batch, length,
     heads_kv, head_dim)``, any strides with a unit last one (pass
     ``cache.transpose(1, 2)`` for a ``(batch, heads, length, head_dim)``
-    cache).  Sequence ``b`` uses keys ``0 .. n_b - 1`` with ``n_b =
+    cache), or with ``pages`` the pools ``(num_pages, page_size, heads_kv,
+    head_dim)``.  Sequence ``b`` uses keys ``0 .. n_b - 1`` with ``n_b =
     seqused_k[b]`` (int32), ``positions[b] + 1`` (int64) or ``length``.
     ``workspace`` defaults to the device's shared one.  Returns ``(batch, heads_q, head_dim)``.
     """
@@ -362,7 +405,7 @@ def decode(
             f"decode expects q (B, Hq, D) and k/v (B, L, Hkv, D); got {tuple(q.shape)}, "
             f"{tuple(k.shape)}, {tuple(v.shape)}"
         )
-    if k.shape[0] != q.shape[0] or k.shape[3] != q.shape[2]:
+    if (pages is None and k.shape[0] != q.shape[0]) or k.shape[3] != q.shape[2]:
         raise ValueError("q and k disagree on batch or head_dim")
     if q.shape[1] % k.shape[2]:
         raise ValueError(f"{q.shape[1]} query heads are not a multiple of {k.shape[2]} kv heads")
@@ -382,19 +425,27 @@ def decode(
     for lengths in (seqused_k, positions):
         if lengths is not None and lengths.shape != (q.shape[0],):
             raise ValueError(f"key counts must have shape ({q.shape[0]},), got {tuple(lengths.shape)}")
-    device = _check_device(q, k, v, out, seqused_k, positions)
+    device = _check_device(q, k, v, out, seqused_k, positions, None if pages is None else pages.block_table)
     params = _decode_params(q, k, v, out, seqused_k, positions, num_splits, scale)
+    pk = None
+    if pages is not None:
+        pk, params.max_len_k = _paged(pages, k, v, q.shape[0])
+        params.k_batch_stride = params.v_batch_stride = 0
     lib = _lib.load()
     need = lib.asrattn_decode_workspace_size(ctypes.byref(params))
     if need == ctypes.c_size_t(-1).value:
-        _lib.check(lib.asrattn_decode(ctypes.byref(params), None, 0, _stream(device)), "asrattn_decode")
+        need = 0  # invalid parameters: the call below reports why
     if workspace is None and need:
         workspace = decode_workspace(need, device)
     size = 0 if workspace is None else workspace.numel() * workspace.element_size()
-    _lib.check(
-        lib.asrattn_decode(ctypes.byref(params), _ptr(workspace), size, _stream(device)),
-        "asrattn_decode",
-    )
+    if pk is None:
+        status = lib.asrattn_decode(ctypes.byref(params), _ptr(workspace), size, _stream(device))
+        _lib.check(status, "asrattn_decode")
+    else:
+        status = lib.asrattn_decode_paged(
+            ctypes.byref(params), None, ctypes.byref(pk), _ptr(workspace), size, _stream(device)
+        )
+        _lib.check(status, "asrattn_decode_paged")
     return out
 
 
@@ -415,8 +466,10 @@ def decode_append(
     scale: float | None = None,
     out: Tensor | None = None,
     workspace: Tensor | None = None,
+    pages: PageTable | None = None,
 ) -> Tensor:
-    """A decoder step with its prologue fused in (``asrattn_decode_append``):
+    """A decoder step with its prologue fused in (``asrattn_decode_append``;
+    with ``pages``, ``k``/``v`` are page pools as for :func:`decode`):
     q ``(batch, heads_q, head_dim)`` and the step's key ``k_new`` ``(batch,
     heads_kv, head_dim)`` get the per-head RMSNorm (``q_norm``/``k_norm``
     weights ``(head_dim,)``, or neither) and the rotary embedding (``cos``/
@@ -432,7 +485,7 @@ def decode_append(
             f"decode_append expects q (B, Hq, D) and k/v (B, L, Hkv, D); got {tuple(q.shape)}, "
             f"{tuple(k.shape)}, {tuple(v.shape)}"
         )
-    batch, heads_kv, head_dim = k.shape[0], k.shape[2], k.shape[3]
+    batch, heads_kv, head_dim = q.shape[0] if pages is not None else k.shape[0], k.shape[2], k.shape[3]
     if q.shape[0] != batch or q.shape[2] != head_dim or q.shape[1] % heads_kv:
         raise ValueError("q and k disagree on batch, head_dim or head grouping")
     for name, t in (("k_new", k_new), ("v_new", v_new)):
@@ -464,8 +517,13 @@ def decode_append(
     elif out.shape != q.shape or out.dtype != q.dtype or out.stride(-1) != 1:
         raise ValueError("out must match q's shape and dtype, with a unit last stride")
     positions = positions.contiguous()
-    device = _check_device(q, k, v, out, positions, k_new, v_new, *extras)
+    device = _check_device(q, k, v, out, positions, k_new, v_new, *extras,
+                           None if pages is None else pages.block_table)
     params = _decode_params(q, k, v, out, None, positions, num_splits, scale)
+    pk = None
+    if pages is not None:
+        pk, params.max_len_k = _paged(pages, k, v, batch)
+        params.k_batch_stride = params.v_batch_stride = 0
     app = _lib.AppendParams()
     app.k_new, app.v_new = k_new.data_ptr(), v_new.data_ptr()
     app.kn_batch_stride, app.kn_head_stride = k_new.stride(0), k_new.stride(1)
@@ -480,10 +538,14 @@ def decode_append(
     if workspace is None and need and need != ctypes.c_size_t(-1).value:
         workspace = decode_workspace(need, device)
     size = 0 if workspace is None else workspace.numel() * workspace.element_size()
-    _lib.check(
-        lib.asrattn_decode_append(ctypes.byref(params), ctypes.byref(app), _ptr(workspace), size, _stream(device)),
-        "asrattn_decode_append",
-    )
+    if pk is None:
+        status = lib.asrattn_decode_append(ctypes.byref(params), ctypes.byref(app), _ptr(workspace), size,
+                                           _stream(device))
+        _lib.check(status, "asrattn_decode_append")
+    else:
+        status = lib.asrattn_decode_paged(ctypes.byref(params), ctypes.byref(app), ctypes.byref(pk),
+                                          _ptr(workspace), size, _stream(device))
+        _lib.check(status, "asrattn_decode_paged")
     return out
 
 

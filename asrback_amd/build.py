@@ -8,10 +8,12 @@ PyTorch dependency; it is loaded with ctypes (:mod:`asrback_amd._lib`).
 
 from __future__ import annotations
 
+import concurrent.futures
 import os
 import shutil
 import subprocess
 import sys
+import tempfile
 from pathlib import Path
 
 PACKAGE = Path(__file__).resolve().parent
@@ -45,20 +47,7 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (set HIPCC or install ROCm under /opt/rocm)")
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile every kernel source into ``libasrattn.so`` and return its path."""
-    if not SOURCES:
-        raise RuntimeError(f"no HIP sources under {PACKAGE / 'csrc'}")
-    tmp = LIBRARY.with_suffix(f".so.tmp{os.getpid()}")
-    cmd = [
-        hipcc(),
-        *FLAGS,
-        f"-I{ROOT / 'include'}",
-        f"-I{PACKAGE / 'csrc'}",
-        *map(str, SOURCES),
-        "-o",
-        str(tmp),
-    ]
+def _run(cmd: list[str], verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
     result = subprocess.run(cmd, capture_output=True, text=True)
@@ -68,10 +57,32 @@ def build(verbose: bool = False) -> Path:
         if "packed-fp32-ops" not in line  # the host pass does not know the feature
     )
     if result.returncode != 0:
-        tmp.unlink(missing_ok=True)
         raise RuntimeError(f"hipcc failed ({result.returncode}):\n{output}")
     if verbose and output.strip():
         print(output, flush=True)
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile every kernel source (one hipcc per source, in parallel) and
+    link them into ``libasrattn.so``; return its path."""
+    if not SOURCES:
+        raise RuntimeError(f"no HIP sources under {PACKAGE / 'csrc'}")
+    includes = [f"-I{ROOT / 'include'}", f"-I{PACKAGE / 'csrc'}"]
+    compile_flags = [flag for flag in FLAGS if flag != "-shared"]
+    tmp = LIBRARY.with_suffix(f".so.tmp{os.getpid()}")
+    with tempfile.TemporaryDirectory(prefix="asrattn_build_") as work:
+        objects = [str(Path(work) / (source.stem + ".o")) for source in SOURCES]
+        jobs = [[hipcc(), *compile_flags, *includes, "-c", str(source), "-o", obj]
+                for source, obj in zip(SOURCES, objects)]
+        workers = max(1, min(len(jobs), int(os.environ.get("MAX_JOBS", "0")) or os.cpu_count() or 1))
+        with concurrent.futures.ThreadPoolExecutor(workers) as pool:
+            for future in [pool.submit(_run, job, verbose) for job in jobs]:
+                future.result()
+        try:
+            _run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objects, "-o", str(tmp)], verbose)
+        except BaseException:
+            tmp.unlink(missing_ok=True)
+            raise
     os.replace(tmp, LIBRARY)
     return LIBRARY
 

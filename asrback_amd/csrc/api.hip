@@ -227,8 +227,9 @@ int asrattn_decode_num_splits(const asrattn_decode_params* params) {
 
 namespace {
 
-int run_decode(const asrattn_decode_params* params, const asrattn_append_params* append, void* workspace,
-               size_t workspace_bytes, void* stream, const char* name) {
+int run_decode(const asrattn_decode_params* params, const asrattn_append_params* append,
+               const asrattn_paged_kv* paged, void* workspace, size_t workspace_bytes, void* stream,
+               const char* name) {
   int rc = check_decode(params);
   if (rc != ASRATTN_OK) return rc;
   const asrattn_decode_params& p = *params;
@@ -257,11 +258,30 @@ int run_decode(const asrattn_decode_params* params, const asrattn_append_params*
       return fail(ASRATTN_ERR_INVALID,
                   "k_new, v_new, the norm weights and cos/sin need 16-byte aligned pointers and strides");
   }
-  // Keys are addressed with 32-bit byte offsets from the sequence's start.
   const long long es = p.dtype == ASRATTN_BF16 ? 2 : 4;
-  if ((long long)p.max_len_k * p.k_token_stride * es >= (1LL << 31) ||
-      (long long)p.max_len_k * p.v_token_stride * es >= (1LL << 31))
+  if (paged != nullptr) {
+    const asrattn_paged_kv& pk = *paged;
+    const int min_page = 4 * asrattn::decode_keys_per_wave(p.dtype, p.head_dim);
+    if (pk.block_table == nullptr) return fail(ASRATTN_ERR_INVALID, "block_table must be non-NULL");
+    if (pk.page_size < 16 || (pk.page_size & (pk.page_size - 1)) != 0 || pk.page_size < min_page)
+      return fail(ASRATTN_ERR_UNSUPPORTED, "page_size must be a power of two >= %d for this dtype and head_dim, got %d",
+                  min_page < 16 ? 16 : min_page, pk.page_size);
+    if (pk.num_pages < 0 || pk.bt_stride < 1)
+      return fail(ASRATTN_ERR_INVALID, "num_pages must be >= 0 and bt_stride >= 1");
+    if ((long long)p.max_len_k > pk.bt_stride * (long long)pk.page_size)
+      return fail(ASRATTN_ERR_INVALID, "max_len_k (%d) exceeds the block table's reach (%lld pages of %d)", p.max_len_k,
+                  (long long)pk.bt_stride, pk.page_size);
+    if (!vec_aligned(p.k, p.dtype, {pk.k_page_stride}) || !vec_aligned(p.v, p.dtype, {pk.v_page_stride}))
+      return fail(ASRATTN_ERR_INVALID, "page strides must be multiples of 16 bytes");
+    // Keys are addressed with 32-bit byte offsets from their page's start.
+    if ((long long)pk.page_size * p.k_token_stride * es >= (1LL << 31) ||
+        (long long)pk.page_size * p.v_token_stride * es >= (1LL << 31))
+      return fail(ASRATTN_ERR_UNSUPPORTED, "one page spans 2 GiB or more");
+  } else if ((long long)p.max_len_k * p.k_token_stride * es >= (1LL << 31) ||
+             (long long)p.max_len_k * p.v_token_stride * es >= (1LL << 31)) {
+    // Keys are addressed with 32-bit byte offsets from the sequence's start.
     return fail(ASRATTN_ERR_UNSUPPORTED, "one sequence's keys span 2 GiB or more");
+  }
   const int s = decode_splits(p);
   const DecodeWorkspace w = decode_workspace(p, s);
   float* ws_o = nullptr;
@@ -276,13 +296,13 @@ int run_decode(const asrattn_decode_params* params, const asrattn_append_params*
     ws_o = reinterpret_cast<float*>(base + w.partials);
     ws_ml = reinterpret_cast<float*>(base + w.stats);
   }
-  return from_hip(asrattn::launch_decode(p, append, s, ws_o, ws_ml, static_cast<hipStream_t>(stream)), name);
+  return from_hip(asrattn::launch_decode(p, append, paged, s, ws_o, ws_ml, static_cast<hipStream_t>(stream)), name);
 }
 
 }  // namespace
 
 int asrattn_decode(const asrattn_decode_params* params, void* workspace, size_t workspace_bytes, void* stream) {
-  return run_decode(params, nullptr, workspace, workspace_bytes, stream, "asrattn_decode");
+  return run_decode(params, nullptr, nullptr, workspace, workspace_bytes, stream, "asrattn_decode");
 }
 
 int asrattn_choose(const float* logits, int64_t rows, int64_t vocab, int64_t row_stride, const uint8_t* suppress,
@@ -302,7 +322,13 @@ int asrattn_choose(const float* logits, int64_t rows, int64_t vocab, int64_t row
 int asrattn_decode_append(const asrattn_decode_params* params, const asrattn_append_params* append,
                           void* workspace, size_t workspace_bytes, void* stream) {
   if (append == nullptr) return fail(ASRATTN_ERR_INVALID, "append parameters must be non-NULL");
-  return run_decode(params, append, workspace, workspace_bytes, stream, "asrattn_decode_append");
+  return run_decode(params, append, nullptr, workspace, workspace_bytes, stream, "asrattn_decode_append");
+}
+
+int asrattn_decode_paged(const asrattn_decode_params* params, const asrattn_append_params* append,
+                         const asrattn_paged_kv* paged, void* workspace, size_t workspace_bytes, void* stream) {
+  if (paged == nullptr) return fail(ASRATTN_ERR_INVALID, "paged parameters must be non-NULL");
+  return run_decode(params, append, paged, workspace, workspace_bytes, stream, "asrattn_decode_paged");
 }
 
 }  // extern "C"

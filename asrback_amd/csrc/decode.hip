@@ -25,6 +25,13 @@
 //
 // Softmax runs in base 2: each reduced score q . k is multiplied by
 // scale * log2(e), so p = 2^(s - max) on v_exp_f32.
+//
+// Paged caches (asrattn_decode_paged): a load batch is U slices of NS
+// consecutive keys (one key per stream), NS-aligned; with page sizes that
+// are multiples of NS each slice lies in one page, whose pool index is one
+// uniform (scalar) load from the block table.  The slice's buffer resource
+// starts at that page and ends at the sequence's last key in it, so unused
+// page slots and pages past the sequence are never read.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -34,6 +41,8 @@ namespace {
 struct DecodeArgs {
   asrattn_decode_params p;
   asrattn_append_params ap;  // the fused prologue (append variant only)
+  asrattn_paged_kv pk;       // the page table (paged variant only)
+  int page_shift;            // log2(pk.page_size)
   float* ws_o;   // [batch][heads_q][splits][head_dim]
   float* ws_ml;  // [batch][heads_q][splits][2]
   int splits;
@@ -266,7 +275,7 @@ struct Stream {
 // split folds them into its state); the first split writes them to the
 // cache at positions[b].  No workgroup reads that slot, so splits need no
 // ordering among themselves.
-template <typename T, int HD, int G, int W, bool APPEND>
+template <typename T, int HD, int G, int W, bool APPEND, bool PAGED>
 __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeArgs a) {
   using S = DecodeShape<T, HD, G, W>;
   constexpr int EPL = S::kEPL, LPK = S::kLPK, NS = S::kStreams, U = S::kUnroll, STEP = S::kStep;
@@ -283,7 +292,8 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeArgs a) {
   const int64_t pos = APPEND ? p.positions[b] : 0;
   const int n = APPEND ? (int)min(max(pos, (int64_t)0), (int64_t)p.max_len_k)
                        : decode_key_count(p.seqused_k, p.positions, b, p.max_len_k);
-  const int chunk = (n + a.splits - 1) / a.splits;
+  int chunk = (n + a.splits - 1) / a.splits;
+  if constexpr (PAGED) chunk = (chunk + NS - 1) / NS * NS;  // slices stay inside pages
   const int k0 = min(n, split * chunk);
   const int k1 = min(n, k0 + chunk);
 
@@ -325,15 +335,27 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeArgs a) {
   // K and V of this (sequence, kv head) through buffer resources that end
   // at the split's last key: loads past it return zeros without a branch,
   // so the two load batches stay in flight across the loop.
-  const char* kbase = reinterpret_cast<const char*>(static_cast<const T*>(p.k) + (int64_t)b * p.k_batch_stride +
-                                                    (int64_t)hkv * p.k_head_stride);
-  const char* vbase = reinterpret_cast<const char*>(static_cast<const T*>(p.v) + (int64_t)b * p.v_batch_stride +
-                                                    (int64_t)hkv * p.v_head_stride);
+  // (Paged: the pool, past the sequence's first page.)
+  const int64_t kbatch = PAGED ? 0 : (int64_t)b * p.k_batch_stride;
+  const int64_t vbatch = PAGED ? 0 : (int64_t)b * p.v_batch_stride;
+  const char* kbase =
+      reinterpret_cast<const char*>(static_cast<const T*>(p.k) + kbatch + (int64_t)hkv * p.k_head_stride);
+  const char* vbase =
+      reinterpret_cast<const char*>(static_cast<const T*>(p.v) + vbatch + (int64_t)hkv * p.v_head_stride);
   const uint32_t kts = (uint32_t)(p.k_token_stride * (int64_t)sizeof(T));
   const uint32_t vts = (uint32_t)(p.v_token_stride * (int64_t)sizeof(T));
   const __amdgpu_buffer_rsrc_t krs = buffer_rsrc(kbase, (uint32_t)k1 * kts);
   const __amdgpu_buffer_rsrc_t vrs = buffer_rsrc(vbase, (uint32_t)k1 * vts);
   const uint32_t lane_bytes = sub * EPL * (uint32_t)sizeof(T);
+
+  // Paged: pool page of logical page pi of this sequence, or -1 when the
+  // entry is missing or outside the pool (its keys are skipped).
+  const int32_t* bt = PAGED ? a.pk.block_table + (int64_t)b * a.pk.bt_stride : nullptr;
+  auto pool_page = [&](int pi) -> int {
+    if (pi >= a.pk.bt_stride) return -1;
+    const int e = bt[__builtin_amdgcn_readfirstlane(pi)];
+    return e >= 0 && e < a.pk.num_pages ? e : -1;
+  };
 
   // Key u of the batch starting at `base` is base + u * NS + stream.
   auto load = [&](uint4* kr, uint4* vr, int base) -> unsigned {
@@ -341,9 +363,23 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeArgs a) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int j = base + u * NS + stream;
-      kr[u] = buffer_load16(krs, (uint32_t)j * kts + lane_bytes);
-      vr[u] = buffer_load16(vrs, (uint32_t)j * vts + lane_bytes);
-      mask |= (j < k1 ? 1u : 0u) << u;
+      if constexpr (PAGED) {
+        const int j0 = base + u * NS;  // uniform; the slice lies in one page
+        const int pi = j0 >> a.page_shift;
+        const int first = pi << a.page_shift;
+        const int page = pool_page(pi);
+        const uint32_t keys = page >= 0 ? (uint32_t)min(max(k1 - first, 0), a.pk.page_size) : 0u;
+        const int64_t pg = page >= 0 ? page : 0;
+        const __amdgpu_buffer_rsrc_t kp = buffer_rsrc(kbase + pg * a.pk.k_page_stride * (int64_t)sizeof(T), keys * kts);
+        const __amdgpu_buffer_rsrc_t vp = buffer_rsrc(vbase + pg * a.pk.v_page_stride * (int64_t)sizeof(T), keys * vts);
+        kr[u] = buffer_load16(kp, (uint32_t)(j - first) * kts + lane_bytes);
+        vr[u] = buffer_load16(vp, (uint32_t)(j - first) * vts + lane_bytes);
+        mask |= (j < k1 && page >= 0 ? 1u : 0u) << u;
+      } else {
+        kr[u] = buffer_load16(krs, (uint32_t)j * kts + lane_bytes);
+        vr[u] = buffer_load16(vrs, (uint32_t)j * vts + lane_bytes);
+        mask |= (j < k1 ? 1u : 0u) << u;
+      }
     }
     return mask;
   };
@@ -372,8 +408,20 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeArgs a) {
 
   if constexpr (APPEND) {
     if (split == 0 && stream == 0 && pos >= 0 && pos < p.max_len_k) {
-      *reinterpret_cast<uint4*>(const_cast<char*>(kbase) + (int64_t)pos * kts + lane_bytes) = knew;
-      *reinterpret_cast<uint4*>(const_cast<char*>(vbase) + (int64_t)pos * vts + lane_bytes) = vnew;
+      int64_t koff = pos * kts, voff = pos * vts;
+      bool write = true;
+      if constexpr (PAGED) {
+        const int pi = (int)(pos >> a.page_shift);
+        const int page = pool_page(pi);
+        const int64_t slot = pos - ((int64_t)pi << a.page_shift);
+        write = page >= 0;
+        koff = (int64_t)page * a.pk.k_page_stride * (int64_t)sizeof(T) + slot * kts;
+        voff = (int64_t)page * a.pk.v_page_stride * (int64_t)sizeof(T) + slot * vts;
+      }
+      if (write) {
+        *reinterpret_cast<uint4*>(const_cast<char*>(kbase) + koff + lane_bytes) = knew;
+        *reinterpret_cast<uint4*>(const_cast<char*>(vbase) + voff + lane_bytes) = vnew;
+      }
     }
   }
 
@@ -450,10 +498,15 @@ template <typename T, int HD, int G, int W>
 hipError_t launch_typed(const DecodeArgs& a, bool append, hipStream_t stream) {
   const asrattn_decode_params& p = a.p;
   dim3 grid(a.splits, p.heads_kv, p.batch);
-  if (append)
-    hipLaunchKernelGGL((decode_kernel<T, HD, G, W, true>), grid, dim3(64 * W), 0, stream, a);
+  const bool paged = a.pk.block_table != nullptr;
+  if (append && paged)
+    hipLaunchKernelGGL((decode_kernel<T, HD, G, W, true, true>), grid, dim3(64 * W), 0, stream, a);
+  else if (append)
+    hipLaunchKernelGGL((decode_kernel<T, HD, G, W, true, false>), grid, dim3(64 * W), 0, stream, a);
+  else if (paged)
+    hipLaunchKernelGGL((decode_kernel<T, HD, G, W, false, true>), grid, dim3(64 * W), 0, stream, a);
   else
-    hipLaunchKernelGGL((decode_kernel<T, HD, G, W, false>), grid, dim3(64 * W), 0, stream, a);
+    hipLaunchKernelGGL((decode_kernel<T, HD, G, W, false, false>), grid, dim3(64 * W), 0, stream, a);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || a.splits == 1) return err;
   hipLaunchKernelGGL((decode_combine_kernel<T, HD>), dim3(p.heads_q, p.batch), dim3(HD), 0, stream, a);
@@ -488,7 +541,11 @@ bool decode_supported(int dtype, int head_dim, int group) {
   return dt && hd && g;
 }
 
-int decode_waves(const asrattn_decode_params& p, int splits) {
+int decode_keys_per_wave(int dtype, int head_dim) {
+  return 64 / (head_dim * (dtype == ASRATTN_BF16 ? 2 : 4) / 16);
+}
+
+int decode_waves(const asrattn_decode_params& p, int splits, int page_size) {
   // Enough waves in flight to keep HBM busy: about 16 per CU over the grid,
   // but no more waves than key rows a load batch can use.
   const long long groups = (long long)p.batch * p.heads_kv * splits;
@@ -497,21 +554,26 @@ int decode_waves(const asrattn_decode_params& p, int splits) {
   // A wave loads 64 / LPK rows per instruction (8 for bf16 x 64, 4 for 128).
   const int rows_per_wave = 64 / (p.head_dim * (p.dtype == ASRATTN_BF16 ? 2 : 4) / 16);
   while (waves > 4 && waves * rows_per_wave * 2 > keys_per_split) waves /= 2;
+  // Paged: a slice (one key per stream of the workgroup) within one page.
+  while (page_size > 0 && waves > 4 && waves * rows_per_wave > page_size) waves /= 2;
   return waves;
 }
 
-hipError_t launch_decode(const asrattn_decode_params& p, const asrattn_append_params* append, int splits,
-                         float* ws_o, float* ws_ml, hipStream_t stream) {
+hipError_t launch_decode(const asrattn_decode_params& p, const asrattn_append_params* append,
+                         const asrattn_paged_kv* paged, int splits, float* ws_o, float* ws_ml, hipStream_t stream) {
   DecodeArgs a;
   a.p = p;
   a.ap = append != nullptr ? *append : asrattn_append_params{};
+  a.pk = paged != nullptr ? *paged : asrattn_paged_kv{};
+  a.page_shift = 0;
+  while (paged != nullptr && (1 << a.page_shift) < paged->page_size) ++a.page_shift;
   const bool app = append != nullptr;
   a.ws_o = ws_o;
   a.ws_ml = ws_ml;
   a.splits = splits;
   a.c = p.scale * kLog2e;
   const int group = p.heads_q / p.heads_kv;
-  const int waves = decode_waves(p, splits);
+  const int waves = decode_waves(p, splits, paged != nullptr ? paged->page_size : 0);
   if (p.dtype == ASRATTN_BF16) {
     return p.head_dim == 64 ? launch_hd<bf16_raw, 64>(a, group, waves, app, stream)
                             : launch_hd<bf16_raw, 128>(a, group, waves, app, stream);

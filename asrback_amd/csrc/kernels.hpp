@@ -13,10 +13,14 @@ namespace asrattn {
 // splits > 1 the workspace holds the partial outputs
 // float[batch][heads_q][splits][head_dim] and (max, sum) pairs
 // float[batch][heads_q][splits][2], merged by a second kernel.
-// append: the fused prologue of asrattn_decode_append, or null.
-hipError_t launch_decode(const asrattn_decode_params& p, const asrattn_append_params* append, int splits,
-                         float* ws_o, float* ws_ml, hipStream_t stream);
-int decode_waves(const asrattn_decode_params& p, int splits);
+// append: the fused prologue of asrattn_decode_append, or null; paged: the
+// page table of asrattn_decode_paged, or null.
+hipError_t launch_decode(const asrattn_decode_params& p, const asrattn_append_params* append,
+                         const asrattn_paged_kv* paged, int splits, float* ws_o, float* ws_ml, hipStream_t stream);
+// Waves per workgroup (page_size 0: not paged) and key rows one wave load
+// covers.
+int decode_waves(const asrattn_decode_params& p, int splits, int page_size);
+int decode_keys_per_wave(int dtype, int head_dim);
 bool decode_supported(int dtype, int head_dim, int group);
 
 // Multi-row forward on matrix cores with K/V streamed into an LDS ring by

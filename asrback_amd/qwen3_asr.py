@@ -19,6 +19,11 @@ decode loop around them (``DecodeState``, ``choose``, ``TextGreedyDecoder``:
   reference's ``mask`` in both of its forms -- the varlen tuple
   ``(query_starts, key_starts, lengths)`` and the boolean ``(batch, 1, 1,
   length)`` mask -- and a :class:`~asrback_amd.attention.KeyPrefix`.
+* :class:`PagedKVCache` replaces the fixed 1024-slot rows with pages from a
+  shared pool and a block table (``TextGreedyDecoder(page_size=...)``):
+  rows hold the pages their prompt and generation limit need.  Its layers
+  index like the slab (``keys[rows, positions] = k``), so the attention
+  modules take either cache.
 """
 
 from __future__ import annotations
@@ -31,7 +36,7 @@ import torch
 import torch.nn.functional as F
 from torch import Tensor, nn
 
-from .attention import KeyPrefix, decode, decode_append, greedy_choice, varlen_attn
+from .attention import KeyPrefix, PageTable, decode, decode_append, greedy_choice, varlen_attn
 from .transcription import CapturedGraph, to_device
 
 # Positions per row of the KV cache (qwen3_asr.py:57-59).
@@ -138,6 +143,91 @@ class KVCache:
         return KVCache(self.keys[:, :batch_size, :length], self.values[:, :batch_size, :length])
 
 
+class PagedLayer:
+    """One layer's keys (or values) of a :class:`PagedKVCache`, addressed as
+    the slab ``(batch, length, kv_heads, head_dim)`` would be: ``layer[rows,
+    positions] = x`` writes each token to its row's page."""
+
+    def __init__(self, pool: Tensor, table: PageTable, page_size: int) -> None:
+        self.pool = pool  # (num_pages, page_size, kv_heads, head_dim)
+        self.table = table
+        self.page_size = page_size
+        self.dtype = pool.dtype
+        self.device = pool.device
+        batch, reach = table.block_table.shape[0], table.max_len
+        self.shape = (batch, reach, pool.shape[2], pool.shape[3])
+
+    def __setitem__(self, index: tuple[Tensor, Tensor], value: Tensor) -> None:
+        rows, positions = index
+        pages = self.table.block_table[rows, positions // self.page_size].long()
+        self.pool[pages, positions % self.page_size] = value
+
+
+@dataclass
+class PagedKVCache:
+    """Keys and values in pages of ``page_size`` positions from one pool per
+    layer, ``(layers, num_pages, page_size, kv_heads, head_dim)``, and a block
+    table ``(batch, CACHE_LENGTH / page_size)`` (int32, on the device; -1 for
+    no page) mapping each row's logical pages to pool pages.  Generalizes the
+    reference's ``row * 1024`` slab (``qwen3_asr.py:511-512``): a row holds
+    only the pages its keys need, so the pool -- not ``CACHE_LENGTH`` times
+    the batch -- bounds how many rows fit.  Pages are handed out on the host
+    (:meth:`assign`, :meth:`release`); the tensors keep fixed addresses."""
+
+    pool_keys: Tensor
+    pool_values: Tensor
+    block_table: Tensor
+    page_size: int
+    free_pages: list[int]
+
+    @classmethod
+    def allocate(cls, config: dict, batch: int, num_pages: int, page_size: int, device, dtype) -> PagedKVCache:
+        if CACHE_LENGTH % page_size:
+            raise ValueError(f"page_size must divide {CACHE_LENGTH}")
+        shape = (config["num_hidden_layers"], num_pages, page_size, config["num_key_value_heads"], config["head_dim"])
+        table = torch.full((batch, CACHE_LENGTH // page_size), -1, dtype=torch.int32, device=device)
+        return cls(torch.zeros(shape, dtype=dtype, device=device), torch.zeros(shape, dtype=dtype, device=device),
+                   table, page_size, list(range(num_pages - 1, -1, -1)))
+
+    def __post_init__(self) -> None:
+        # Per layer, indexed like KVCache.keys / .values.
+        table = PageTable(self.block_table, CACHE_LENGTH)
+        self.keys = [PagedLayer(pool, table, self.page_size) for pool in self.pool_keys]
+        self.values = [PagedLayer(pool, table, self.page_size) for pool in self.pool_values]
+
+    def narrow(self, batch_size: int, length: int) -> PagedKVCache:
+        del length  # every row reads only its own pages
+        return PagedKVCache(self.pool_keys, self.pool_values, self.block_table[:batch_size], self.page_size,
+                            self.free_pages)
+
+    def pages_for(self, positions: int) -> int:
+        return -(-positions // self.page_size)
+
+    def assign(self, row: int, positions: int) -> list[int]:
+        """Pages for positions ``0 .. positions - 1`` of ``row`` (whose
+        previous pages must have been released)."""
+        count = self.pages_for(positions)
+        if count > len(self.free_pages):
+            raise RuntimeError(f"paged cache exhausted: {count} pages wanted, {len(self.free_pages)} free")
+        pages = [self.free_pages.pop() for _ in range(count)]
+        entries = torch.full((self.block_table.shape[1],), -1, dtype=torch.int32)
+        entries[:count] = torch.tensor(pages, dtype=torch.int32)
+        self.block_table[row].copy_(entries.to(self.block_table.device))
+        return pages
+
+    def release(self, row: int, pages: list[int]) -> None:
+        self.block_table[row].fill_(-1)
+        self.free_pages.extend(reversed(pages))
+
+
+def _cache_layer(layer) -> tuple[Tensor, PageTable | None]:
+    """The tensor the kernels read for one layer's keys or values, and its
+    page table (None for the slab)."""
+    if isinstance(layer, PagedLayer):
+        return layer.pool, layer.table
+    return layer, None
+
+
 def _step_lengths(mask, positions: Tensor, length: int) -> Tensor:
     """Keys per row for a decoder step from any of the reference's mask forms."""
     if isinstance(mask, KeyPrefix):
@@ -196,16 +286,18 @@ class TextAttention(nn.Module):
         passes), the norms, the rotation, the cache write and the attention
         run as one kernel (:func:`~asrback_amd.attention.decode_append`);
         other mask forms take the reference's sequence of ops."""
-        if isinstance(mask, KeyPrefix) and mask.positions is positions and self._fused_step(x, keys):
+        key_cache, pages = _cache_layer(keys)
+        value_cache, _ = _cache_layer(values)
+        if isinstance(mask, KeyPrefix) and mask.positions is positions and self._fused_step(x, key_cache):
             batch = len(x)
             q, k, v = self.qkv_proj(x).split(self.sizes, dim=-1)
             output = decode_append(
                 q.view(batch, self.heads, self.head_dim),
                 k.view(batch, self.kv_heads, self.head_dim),
                 v.view(batch, self.kv_heads, self.head_dim),
-                keys, values, positions,
+                key_cache, value_cache, positions,
                 q_norm=self.q_norm.weight, k_norm=self.k_norm.weight, eps=self.q_norm.eps,
-                cos=cos, sin=sin,
+                cos=cos, sin=sin, pages=pages,
             )
             return self.o_proj(output.flatten(1))
         q, k, v = self._project(x, cos, sin)
@@ -213,7 +305,7 @@ class TextAttention(nn.Module):
         keys[rows, positions] = k
         values[rows, positions] = v
         lengths = _step_lengths(mask, positions, keys.shape[1])
-        output = decode(q, keys, values, seqused_k=lengths)
+        output = decode(q, key_cache, value_cache, seqused_k=lengths, pages=pages)
         return self.o_proj(output.flatten(1))
 
 
@@ -340,11 +432,15 @@ class TextGreedyDecoder:
     :meth:`finished_rows` returns and frees finished rows (``_finish``,
     ``:1131-1155``).  Attention reads each row's own keys, so one KV bucket
     (the whole 1024-position slab) serves every length, as with the
-    reference's varlen path.
+    reference's varlen path.  With ``page_size`` the cache is a
+    :class:`PagedKVCache` of ``num_pages`` pages (default: as many
+    positions as the slab): a row holds the pages for its prompt and its
+    generation limit from admission until it finishes.
     """
 
     def __init__(self, text: TextModel, lm_head: nn.Module, config: dict, max_batch_size: int,
-                 eos_ids: list[int], graphs: bool = True) -> None:
+                 eos_ids: list[int], graphs: bool = True, page_size: int | None = None,
+                 num_pages: int | None = None) -> None:
         self.text = text
         self.lm_head = lm_head
         self.config = config
@@ -356,7 +452,11 @@ class TextGreedyDecoder:
             {min(2**p, max_batch_size) for p in range(max_batch_size.bit_length())} | {max_batch_size}
         )
         self.kv_buckets = [CACHE_LENGTH]
-        self.cache = KVCache.allocate(config, max_batch_size, CACHE_LENGTH, self.device, self.dtype)
+        if page_size is None:
+            self.cache = KVCache.allocate(config, max_batch_size, CACHE_LENGTH, self.device, self.dtype)
+        else:
+            pages = max_batch_size * CACHE_LENGTH // page_size if num_pages is None else num_pages
+            self.cache = PagedKVCache.allocate(config, max_batch_size, pages, page_size, self.device, self.dtype)
         self.state = DecodeState.allocate(max_batch_size, self.device)
         self.eos_ids = torch.tensor(eos_ids, dtype=torch.long, device=self.device)
         self.rows: dict[int, dict] = {}
@@ -407,6 +507,13 @@ class TextGreedyDecoder:
         limits = [min(n, CACHE_LENGTH - length) for n, length in zip(max_new_tokens, lengths)]
         ends = [length - 1 + limit for length, limit in zip(lengths, limits)]
         audio = np.flatnonzero(ids == audio_id) if audio_id is not None else None
+        if isinstance(self.cache, PagedKVCache):
+            wanted = sum(self.cache.pages_for(end + 1) for end in ends)
+            if wanted > len(self.cache.free_pages):
+                raise RuntimeError(f"paged cache exhausted: {wanted} pages wanted, {len(self.cache.free_pages)} free")
+            held = [self.cache.assign(slot, end + 1) for slot, end in zip(slots, ends)]
+        else:
+            held = [[] for _ in slots]
         ids_d, rows, positions_d, slot_rows, start, end = (
             to_device(data, self.device)
             for data in (ids, np.repeat(slots, lengths), positions, slots, lengths, ends)
@@ -426,8 +533,8 @@ class TextGreedyDecoder:
         state.finished[slot_rows] = torch.isin(token, self.eos_ids) | (start >= end)
         state.sum_logprobs[slot_rows] = logprob
         state.generated[slot_rows, start] = token
-        for slot, length, end_position in zip(slots, lengths, ends):
-            self.rows[slot] = {"prompt_length": length, "end": end_position, "bound": length}
+        for slot, length, end_position, pages in zip(slots, lengths, ends, held):
+            self.rows[slot] = {"prompt_length": length, "end": end_position, "bound": length, "pages": pages}
         return slots
 
     def step(self, state: DecodeState, cache: KVCache, temperatures: Tensor | None = None) -> None:
@@ -485,6 +592,8 @@ class TextGreedyDecoder:
         out = {}
         for slot, position, total, tokens in zip(done, positions, sums, generated):
             row = self.rows.pop(slot)
+            if isinstance(self.cache, PagedKVCache):
+                self.cache.release(slot, row["pages"])
             tokens = tokens[row["prompt_length"] : position + 1]
             if tokens and tokens[-1] in eos:
                 tokens.pop()

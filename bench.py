@@ -11,7 +11,8 @@ sum_b 4 * L_b^2 * 512 per layer over valid queries x valid keys.
 
 Decode is reported beside it (``decode``): Qwen3-ASR-1.7B's GQA decoder step
 (28 layers, 16 query / 8 kv heads x 128, batch 64, prompts of 400-430 tokens,
-a (28, 64, 1024, 8, 128) cache, 128 steps) and Whisper-small's decoder step
+a (28, 64, 1024, 8, 128) cache, 128 steps; also over a paged cache of
+64-position pages holding only what the rows use) and Whisper-small's decoder step
 (12 layers, 12 heads x 64, batch 16, self keys 1-224, cross-attention over
 1500 frames), in algorithmic HBM GB/s (K and V of the keys each row uses,
 plus q and o), and the Qwen3 step with its prologue (per-head RMSNorm and
@@ -219,7 +220,7 @@ class Qwen3Decode(Workload):
     bound = "hbm"
     kernel = "decode_kernel"
 
-    def __init__(self, torch, attention, seed: int = 3, steps: int = 128) -> None:
+    def __init__(self, torch, attention, seed: int = 3, steps: int = 128, slab: bool = True) -> None:
         rng = np.random.default_rng(seed)
         self.torch = torch
         self.batch, self.heads_q, self.heads_kv, self.head_dim, self.layers = 64, 16, 8, 128, 28
@@ -227,8 +228,9 @@ class Qwen3Decode(Workload):
         self.prompts = (390 + rng.integers(10, 41, size=self.batch)).astype(np.int64)
         shape = (self.layers, self.batch, self.cache_length, self.heads_kv, self.head_dim)
         g = torch.Generator(device="cuda").manual_seed(seed)
-        self.keys = torch.randn(shape, generator=g, device="cuda", dtype=torch.bfloat16)
-        self.values = torch.randn(shape, generator=g, device="cuda", dtype=torch.bfloat16)
+        if slab:
+            self.keys = torch.randn(shape, generator=g, device="cuda", dtype=torch.bfloat16)
+            self.values = torch.randn(shape, generator=g, device="cuda", dtype=torch.bfloat16)
         self.q = torch.randn((self.layers, self.batch, self.heads_q, self.head_dim), generator=g, device="cuda",
                              dtype=torch.bfloat16)
         self.out = torch.empty((self.batch, self.heads_q, self.head_dim), device="cuda", dtype=torch.bfloat16)
@@ -260,6 +262,44 @@ class Qwen3Decode(Workload):
         return {"workload": self.name, "batch": self.batch, "heads_q": self.heads_q, "heads_kv": self.heads_kv,
                 "head_dim": self.head_dim, "layers": self.layers, "cache": list(self.keys.shape[1:]),
                 "prompt_tokens": "390 + U{10..40}", "steps": self.steps}
+
+
+class Qwen3DecodePaged(Qwen3Decode):
+    """The Qwen3-ASR-1.7B decode workload over a paged cache: 64-position
+    pages in random pool order, each row holding the pages for its prompt
+    and the 128 steps (9 per row, 576 pages: 56% of the slab's 1024
+    positions per row), the block table read on the device
+    (``asrattn_decode_paged``).  Same prompts, positions and bytes."""
+
+    name = "qwen3-asr-1.7b-decode-attention-paged"
+    page_size = 64
+
+    def __init__(self, torch, attention, seed: int = 3, steps: int = 128) -> None:
+        super().__init__(torch, attention, seed, steps, slab=False)
+        per_row = [-(-(int(p) + steps + 1) // self.page_size) for p in self.prompts]
+        pages = sum(per_row)
+        order = np.random.default_rng(seed + 11).permutation(pages)
+        table = np.full((self.batch, self.cache_length // self.page_size), -1, dtype=np.int32)
+        i = 0
+        for b, count in enumerate(per_row):
+            table[b, :count] = order[i : i + count]
+            i += count
+        shape = (self.layers, pages, self.page_size, self.heads_kv, self.head_dim)
+        g = torch.Generator(device="cuda").manual_seed(seed)
+        self.keys = torch.randn(shape, generator=g, device="cuda", dtype=torch.bfloat16)
+        self.values = torch.randn(shape, generator=g, device="cuda", dtype=torch.bfloat16)
+        self.pages = attention.PageTable(torch.from_numpy(table).cuda(), self.cache_length)
+
+    def run(self) -> None:
+        self.positions.add_(1)
+        self.used.copy_(self.positions + 1)
+        for layer in range(self.layers):
+            self.attention.decode(self.q[layer], self.keys[layer], self.values[layer], seqused_k=self.used,
+                                  out=self.out, pages=self.pages)
+
+    def config(self) -> dict:
+        return {**super().config(), "workload": self.name, "page_size": self.page_size,
+                "pool_pages": int(self.keys.shape[1]), "cache": list(self.keys.shape[1:])}
 
 
 class Qwen3DecodeStepFused(Qwen3Decode):
@@ -648,8 +688,8 @@ def main() -> int:
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--no-cpu-baseline", action="store_true")
-    parser.add_argument("--only", choices=["sensevoice", "sensevoice-fsmn", "turbo", "qwen3", "qwen3-fused",
-                                           "whisper-small", "choice", "copy"],
+    parser.add_argument("--only", choices=["sensevoice", "sensevoice-fsmn", "turbo", "qwen3", "qwen3-paged",
+                                           "qwen3-fused", "whisper-small", "choice", "copy"],
                         default=None,
                         help="measure one workload only (for profiling)")
     parser.add_argument("--sweep", action="store_true",
@@ -680,6 +720,7 @@ def main() -> int:
         "sensevoice-fsmn": SenseVoiceAttentionFsmn,
         "turbo": WhisperTurboEncoder,
         "qwen3": Qwen3Decode,
+        "qwen3-paged": Qwen3DecodePaged,
         "qwen3-fused": Qwen3DecodeStepFused,
         "choice": GreedyChoice,
         "whisper-small": WhisperSmallDecoderStep,
@@ -696,7 +737,7 @@ def main() -> int:
     head = measure(torch, SenseVoiceEncoder(torch, attention), args.steps, args.warmup)
     torch.cuda.empty_cache()
     decode = []
-    for cls in (Qwen3Decode, Qwen3DecodeStepFused, WhisperSmallDecoderStep, GreedyChoice):
+    for cls in (Qwen3Decode, Qwen3DecodePaged, Qwen3DecodeStepFused, WhisperSmallDecoderStep, GreedyChoice):
         log(f"bench: {cls.name}")
         decode.append(measure(torch, cls(torch, attention), args.steps, args.warmup))
         torch.cuda.empty_cache()

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define ASRATTN_ABI_VERSION 3
+#define ASRATTN_ABI_VERSION 4
 
 enum asrattn_status {
   ASRATTN_OK = 0,
@@ -251,6 +251,42 @@ typedef struct asrattn_append_params {
 
 int asrattn_decode_append(const asrattn_decode_params* params, const asrattn_append_params* append,
                           void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * The decoder step over a paged key/value cache: keys live in pages of
+ * page_size tokens taken from one pool, so each sequence holds only the
+ * pages its keys need instead of a fixed max_len_k-slot slab.  Logical page
+ * i of sequence b (its keys i * page_size .. (i + 1) * page_size - 1) is pool
+ * page block_table[b * bt_stride + i]:
+ *
+ *   key j of sequence b, kv head h at
+ *     k + page * k_page_stride + (j % page_size) * k_token_stride + h * k_head_stride,
+ *     page = block_table[b * bt_stride + j / page_size]
+ *
+ * (likewise v); p_params->k/v point at the pool and k/v_batch_stride are
+ * ignored.  Everything else is asrattn_decode (append == NULL) or
+ * asrattn_decode_append (the new key and value are written to the page of
+ * positions[b]); the workspace size is asrattn_decode_workspace_size's.
+ * max_len_k bounds the keys a sequence may use (<= bt_stride * page_size).
+ * Only the entries of pages holding a sequence's keys are read; an entry
+ * outside [0, num_pages) is not dereferenced and its keys are skipped.
+ *
+ * Replaces (generalizes): the flattened (B * 1024, kv_heads, head_dim) slab
+ * with cu_seqlens_k = row * 1024 of the reference's varlen decode
+ *                                    src/asrback/models/qwen3_asr.py:511-512
+ * whose fixed 1024 slots per row (CACHE_LENGTH, qwen3_asr.py:57-59,
+ * allocated at :817-827) bound the batch size.
+ */
+typedef struct asrattn_paged_kv {
+  const int32_t* block_table; /* int32, sequence b's entries at block_table + b * bt_stride */
+  int64_t bt_stride;          /* entries per sequence */
+  int32_t page_size;          /* tokens per page: a power of two >= 16 (>= 32 for bf16 at head_dim 64) */
+  int32_t num_pages;          /* pages in the pool */
+  int64_t k_page_stride, v_page_stride; /* elements between consecutive pool pages */
+} asrattn_paged_kv;
+
+int asrattn_decode_paged(const asrattn_decode_params* params, const asrattn_append_params* append,
+                         const asrattn_paged_kv* paged, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Greedy next token per row of float32 logits, in one pass:

@@ -41,6 +41,7 @@ def test_header_declares_expected_entry_points():
         "asrattn_fwd_fsmn",
         "asrattn_decode",
         "asrattn_decode_append",
+        "asrattn_decode_paged",
         "asrattn_choose",
         "asrattn_decode_workspace_size",
         "asrattn_decode_num_splits",
@@ -86,13 +87,14 @@ def _c_layout(struct: str, fields: list[str]) -> dict[str, int]:
     return {k: int(v) for k, v in (line.split() for line in out.splitlines())}
 
 
-@pytest.mark.parametrize("name", ["FwdParams", "DecodeParams", "AppendParams", "FsmnParams"])
+@pytest.mark.parametrize("name", ["FwdParams", "DecodeParams", "AppendParams", "FsmnParams", "PagedKV"])
 def test_ctypes_structs_match_c_layout(name):
     from asrback_amd import _lib
 
     cls = getattr(_lib, name)
     struct = {"FwdParams": "asrattn_fwd_params", "DecodeParams": "asrattn_decode_params",
-              "AppendParams": "asrattn_append_params", "FsmnParams": "asrattn_fsmn_params"}[name]
+              "AppendParams": "asrattn_append_params", "FsmnParams": "asrattn_fsmn_params",
+              "PagedKV": "asrattn_paged_kv"}[name]
     fields = [f for f, _ in cls._fields_]
     layout = _c_layout(struct, fields)
     assert layout.pop("sizeof") == ctypes.sizeof(cls)
@@ -203,6 +205,42 @@ def test_invalid_fsmn_arguments_are_reported(lib):
     # Nothing to do: no device call, no error.
     m.kernel_size, f.batch = 11, 0
     assert lib.asrattn_fwd_fsmn(ctypes.byref(f), ctypes.byref(m), None) == _lib.OK
+
+
+def test_invalid_paged_arguments_are_reported(lib):
+    """asrattn_decode_paged's checks, before any device call (stand-in
+    pointers, never dereferenced)."""
+    from asrback_amd import _lib
+
+    p = _lib.DecodeParams()
+    p.batch, p.heads_q, p.heads_kv, p.head_dim, p.max_len_k = 2, 4, 2, 128, 1024
+    p.dtype, p.scale = _lib.BF16, 0.125
+    p.q = p.k = p.v = p.out = 4096
+    p.q_batch_stride, p.q_head_stride = 512, 128
+    p.k_token_stride, p.k_head_stride = 256, 128
+    p.v_token_stride, p.v_head_stride = 256, 128
+    p.o_batch_stride, p.o_head_stride = 512, 128
+    pk = _lib.PagedKV()
+    assert lib.asrattn_decode_paged(ctypes.byref(p), None, None, None, 0, None) == _lib.ERR_INVALID
+    assert lib.asrattn_decode_paged(ctypes.byref(p), None, ctypes.byref(pk), None, 0, None) == _lib.ERR_INVALID
+    assert b"block_table" in lib.asrattn_last_error()
+    pk.block_table, pk.bt_stride, pk.num_pages = 8192, 16, 100
+    pk.k_page_stride = pk.v_page_stride = 64 * 256
+    for bad in (0, 8, 48):  # not a power of two >= 16
+        pk.page_size = bad
+        assert lib.asrattn_decode_paged(ctypes.byref(p), None, ctypes.byref(pk), None, 0, None) == _lib.ERR_UNSUPPORTED
+        assert b"page_size" in lib.asrattn_last_error()
+    pk.page_size = 32  # 16 pages of 32 cannot reach 1024 keys
+    assert lib.asrattn_decode_paged(ctypes.byref(p), None, ctypes.byref(pk), None, 0, None) == _lib.ERR_INVALID
+    assert b"reach" in lib.asrattn_last_error()
+    pk.page_size, pk.k_page_stride = 64, 64 * 256 + 4  # page stride not a multiple of 16 bytes
+    assert lib.asrattn_decode_paged(ctypes.byref(p), None, ctypes.byref(pk), None, 0, None) == _lib.ERR_INVALID
+    assert b"page strides" in lib.asrattn_last_error()
+    # bf16 at head_dim 64: a wave covers 8 keys per load, so pages hold >= 32.
+    p.head_dim, p.q_head_stride, p.k_head_stride, p.v_head_stride = 64, 64, 64, 64
+    pk.k_page_stride, pk.page_size, pk.bt_stride = 64 * 256, 16, 64
+    assert lib.asrattn_decode_paged(ctypes.byref(p), None, ctypes.byref(pk), None, 0, None) == _lib.ERR_UNSUPPORTED
+    assert b">= 32" in lib.asrattn_last_error()
 
 
 def test_workspace_size_and_split_choice(lib):

@@ -392,6 +392,116 @@ def test_decode_append_matches_oracle(ops, device, dtype, batch, heads_q, heads_
     assert torch.equal(kd.cpu()[untouched], keys[untouched]) and torch.equal(vd.cpu()[untouched], values[untouched])
 
 
+def _paginate(cache_k, cache_v, needed, page_size, seed, spare=3):
+    """Pools ``(num_pages, page_size, H, D)`` holding each slab row's first
+    ``needed[b]`` positions in randomly placed pages, and the block table
+    (-1 past a row's pages).  Every other pool slot -- the tail of a row's
+    last page and ``spare`` pages no row owns -- holds NaN, which any read
+    of it would carry into the output."""
+    batch, length, heads, hd = cache_k.shape
+    per_row = [-(-int(n) // page_size) for n in needed]
+    total = sum(per_row) + spare
+    order = np.random.default_rng(seed).permutation(total)
+    pool_k = torch.full((total, page_size, heads, hd), float("nan"), dtype=cache_k.dtype)
+    pool_v = torch.full_like(pool_k, float("nan"))
+    table = torch.full((batch, length // page_size), -1, dtype=torch.int32)
+    i = 0
+    for b in range(batch):
+        for page in range(per_row[b]):
+            table[b, page] = int(order[i])
+            lo, hi = page * page_size, min((page + 1) * page_size, int(needed[b]))
+            pool_k[int(order[i]), : hi - lo] = cache_k[b, lo:hi]
+            pool_v[int(order[i]), : hi - lo] = cache_v[b, lo:hi]
+            i += 1
+    return pool_k, pool_v, table
+
+
+@pytest.mark.parametrize(
+    "dtype,hd,heads_q,heads_kv,page,splits,batch",
+    [
+        (torch.bfloat16, 128, 16, 8, 64, 0, 64),
+        (torch.bfloat16, 128, 16, 8, 16, 0, 8),
+        (torch.bfloat16, 128, 16, 8, 256, 0, 3),
+        (torch.bfloat16, 128, 16, 8, 64, 7, 5),
+        (torch.bfloat16, 64, 12, 12, 32, 0, 16),
+        (torch.float32, 128, 16, 8, 16, 0, 4),
+        (torch.float32, 64, 6, 6, 16, 1, 2),
+    ],
+)
+def test_paged_decode_matches_slab_and_oracle(ops, device, dtype, hd, heads_q, heads_kv, page, splits, batch):
+    """Decode over a paged cache (pages in random pool order, NaN in every
+    slot no row owns) against the oracle on the slab it was cut from
+    (qwen3_asr.py:412-432, :511-512); lengths 1, one page exactly, 1023 and
+    random; split counts that do and do not align with pages.  At the
+    Qwen3 batch (64 rows, 64-position pages) the workgroup shape equals the
+    slab's and the output is bit-identical to decode over the slab."""
+    say("paged decode", dtype, hd, heads_q, heads_kv, page, splits, batch)
+    length = 1024
+    rng = np.random.default_rng(80 + batch)
+    lengths = rng.integers(1, length, size=batch).astype(np.int32)
+    lengths[0] = 1
+    if batch > 2:
+        lengths[1], lengths[2] = page, length - 1
+    q = randn(batch, heads_q, hd, seed=81, dtype=dtype)
+    keys = randn(batch, length, heads_kv, hd, seed=82, dtype=dtype)
+    values = randn(batch, length, heads_kv, hd, seed=83, dtype=dtype)
+    pool_k, pool_v, table = _paginate(keys, values, lengths, page, seed=84)
+    used = torch.from_numpy(lengths)
+    ref = oa.qwen_step_attention(q.float(), keys.float(), values.float(),
+                                 oa.qwen_step_mask(used.long() - 1, length))
+    pages = ops.PageTable(table.to(device), length)
+    out = ops.decode(q.to(device), pool_k.to(device), pool_v.to(device), seqused_k=used.to(device),
+                     num_splits=splits, pages=pages)
+    assert torch.isfinite(out).all()
+    assert max_rel_err(out, ref) < TOL[dtype]
+    if batch == 64:
+        slab = ops.decode(q.to(device), keys.to(device), values.to(device), seqused_k=used.to(device))
+        assert torch.equal(out, slab)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_paged_decode_append_matches_slab(ops, device, dtype):
+    """The fused Qwen3 step on a paged cache: the new key and value land in
+    slot positions % page_size of page table[b, positions // page_size] (page
+    starts and ends included), nothing else changes, and the output equals
+    the same step on the slab."""
+    say("paged decode append", dtype)
+    batch, heads_q, heads_kv, hd, length, page, eps = 64, 16, 8, 128, 1024, 64, 1e-6
+    rng = np.random.default_rng(90)
+    positions = torch.from_numpy(rng.integers(0, 1000, size=batch).astype(np.int64))
+    positions[:4] = torch.tensor([0, 63, 64, 1023])
+    q = randn(batch, heads_q, hd, seed=91, dtype=dtype)
+    k_new = randn(batch, heads_kv, hd, seed=92, dtype=dtype)
+    v_new = randn(batch, heads_kv, hd, seed=93, dtype=dtype)
+    keys = randn(batch, length, heads_kv, hd, seed=94, dtype=dtype)
+    values = randn(batch, length, heads_kv, hd, seed=95, dtype=dtype)
+    g = torch.Generator().manual_seed(96)
+    q_w = (torch.rand(hd, generator=g) + 0.5).to(dtype)
+    k_w = (torch.rand(hd, generator=g) + 0.5).to(dtype)
+    cos, sin = oa.rope_tables(1e6, hd, length, dtype)
+    cos, sin = cos[positions].to(device), sin[positions].to(device)
+    pool_k, pool_v, table = _paginate(keys, values, (positions + 1).numpy(), page, seed=97)
+    # The slot the step writes must not hold an old key: poison it too.
+    rows = torch.arange(batch)
+    slots = table[rows, positions // page].long(), positions % page
+    pool_k[slots] = float("nan")
+    pool_v[slots] = float("nan")
+    args = dict(q_norm=q_w.to(device), k_norm=k_w.to(device), eps=eps, cos=cos, sin=sin)
+    kd, vd = keys.to(device), values.to(device)
+    slab = ops.decode_append(q.to(device), k_new.to(device), v_new.to(device), kd, vd, positions.to(device), **args)
+    pk, pv = pool_k.to(device), pool_v.to(device)
+    out = ops.decode_append(q.to(device), k_new.to(device), v_new.to(device), pk, pv, positions.to(device),
+                            pages=ops.PageTable(table.to(device), length), **args)
+    assert torch.equal(out, slab)
+    assert torch.equal(pk.cpu()[slots], kd.cpu()[rows, positions])
+    assert torch.equal(pv.cpu()[slots], v_new)
+    written = torch.zeros(pool_k.shape[:2], dtype=torch.bool)
+    written[slots] = True
+    for before, after in ((pool_k, pk.cpu()), (pool_v, pv.cpu())):
+        before, after = before[~written], after[~written]
+        assert bool(((after == before) | (before.isnan() & after.isnan())).all())
+
+
 def test_decode_append_whisper_cache_without_norm(ops, device):
     """The Whisper step's scatter + attention (whisper.py:224-237) fused, no
     norm or rotation, into a (batch, heads, length, head_dim) cache through

@@ -264,7 +264,7 @@ def test_qwen_audio_attention_windows(device):
     assert max_rel_err(out.cpu(), expected) < 1e-4
 
 
-def _qwen_decoder(device, graphs, eos_ids):
+def _qwen_decoder(device, graphs, eos_ids, **cache):
     from asrback_amd import qwen3_asr as aq
 
     ref, model = qwen_pair(device)
@@ -273,7 +273,7 @@ def _qwen_decoder(device, graphs, eos_ids):
     prompts = [torch.randint(0, QWEN3["vocab_size"], (n,), generator=g).tolist() for n in (37, 52, 29)]
     lm_head = torch.nn.Linear(QWEN3["hidden_size"], QWEN3["vocab_size"], bias=False)
     lm_head.weight.data.copy_(head)
-    decoder = aq.TextGreedyDecoder(model, lm_head.to(device), QWEN3, 4, eos_ids, graphs=graphs)
+    decoder = aq.TextGreedyDecoder(model, lm_head.to(device), QWEN3, 4, eos_ids, graphs=graphs, **cache)
     expected = [oq.greedy_decode(ref, head, QWEN3, p, 12, eos_ids) for p in prompts]
     for e in expected:
         assert e["min_gap"] > 0.1  # far from argmax ties
@@ -311,6 +311,32 @@ def test_qwen_greedy_decoder_staggered_rows(device):
     third = decoder.admit(prompts[2:], 12)
     _drain(decoder, results)
     assert [results[s] for s in first + third] == expected
+
+
+def test_qwen_greedy_decoder_paged_cache(device):
+    """The same windows on a paged cache of 16-position pages, with a pool of
+    only 14 pages (224 positions, against the slab's 4 x 1024): each row
+    holds the pages for its prompt and 12 new tokens, staggered admissions
+    reuse the pages freed by finished rows, and the tokens are the oracle's
+    (qwen3_asr.py:511-512 generalized)."""
+    say("qwen3 greedy decoder, paged cache")
+    decoder, prompts, expected = _qwen_decoder(device, True, [], page_size=16, num_pages=14)
+    cache = decoder.cache
+    first = decoder.admit(prompts[:2], 12)  # (37 + 12) and (52 + 12) positions: 4 + 4 pages
+    assert len(cache.free_pages) == 14 - 8
+    results = {}
+    decoder.advance()
+    with pytest.raises(RuntimeError, match="exhausted"):
+        decoder.admit([prompts[1], prompts[1]], 12)  # 8 pages wanted, 6 free
+    assert len(cache.free_pages) == 6
+    third = decoder.admit(prompts[2:], 12)  # 29 + 12 positions: 3 pages
+    _drain(decoder, results)
+    assert [results[s] for s in first + third] == expected
+    assert sorted(cache.free_pages) == list(range(14)) and bool((cache.block_table == -1).all())
+    again = decoder.admit(prompts, 12)
+    results = {}
+    _drain(decoder, results)
+    assert [results[s] for s in again] == expected
 
 
 def test_qwen_greedy_decoder_eager_equals_graphs(device):
