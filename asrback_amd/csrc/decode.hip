@@ -6,6 +6,7 @@
 // of loads in flight while it consumes the first, and does all arithmetic in
 // registers:
 //
+//   * K and V are read once, with nontemporal loads (no L2 allocation).
 //   * A key row (head_dim elements) is covered by LPK lanes, 16 bytes each;
 //     a wave loads 64 / LPK key rows per instruction, so every load touches
 //     whole rows.  Each group of LPK lanes runs its own online softmax over
@@ -372,12 +373,12 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeArgs a) {
         const int64_t pg = page >= 0 ? page : 0;
         const __amdgpu_buffer_rsrc_t kp = buffer_rsrc(kbase + pg * a.pk.k_page_stride * (int64_t)sizeof(T), keys * kts);
         const __amdgpu_buffer_rsrc_t vp = buffer_rsrc(vbase + pg * a.pk.v_page_stride * (int64_t)sizeof(T), keys * vts);
-        kr[u] = buffer_load16(kp, (uint32_t)(j - first) * kts + lane_bytes);
-        vr[u] = buffer_load16(vp, (uint32_t)(j - first) * vts + lane_bytes);
+        kr[u] = buffer_load16_stream(kp, (uint32_t)(j - first) * kts + lane_bytes);
+        vr[u] = buffer_load16_stream(vp, (uint32_t)(j - first) * vts + lane_bytes);
         mask |= (j < k1 && page >= 0 ? 1u : 0u) << u;
       } else {
-        kr[u] = buffer_load16(krs, (uint32_t)j * kts + lane_bytes);
-        vr[u] = buffer_load16(vrs, (uint32_t)j * vts + lane_bytes);
+        kr[u] = buffer_load16_stream(krs, (uint32_t)j * kts + lane_bytes);
+        vr[u] = buffer_load16_stream(vrs, (uint32_t)j * vts + lane_bytes);
         mask |= (j < k1 ? 1u : 0u) << u;
       }
     }
