@@ -530,17 +530,27 @@ def roofline(workload: Workload, ms_per_step: float, work_per_step: float) -> di
     else:
         achieved = work_per_step / seconds / 1e9
         peak = PEAK_HBM_GBS
-    return {
+    traffic = measured_traffic().get(TRAFFIC_KEYS.get(workload.name, ""), {}).get("bytes_per_launch")
+    line = {
         "bound": workload.bound,
         "achieved": round(achieved, 2),
         "peak": peak,
         "unit": workload.unit,
         "frac": round(achieved / peak, 4),
-        "traffic": measured_traffic().get(TRAFFIC_KEYS.get(workload.name, ""), {}).get("bytes_per_launch"),
+        "traffic": traffic,
         "kernel": workload.kernel,
         "launches_per_step": workload.launches,
         "avg_launch_us": round(ms_per_step * 1e3 / workload.launches, 2),
     }
+    if workload.unit == "TFLOP/s" and traffic:
+        # The attainable rate given the launch's measured HBM traffic: flops
+        # per byte times the HBM peak, capped by the matrix-core peak.
+        intensity = work_per_step / workload.launches / traffic
+        ceiling = min(peak, intensity * PEAK_HBM_GBS / 1e3)
+        line["flop_per_byte"] = round(intensity, 1)
+        line["ceiling"] = round(ceiling, 1)
+        line["frac_of_ceiling"] = round(achieved / ceiling, 4)
+    return line
 
 
 def measure(torch, workload: Workload, steps: int, warmup: int) -> dict:
