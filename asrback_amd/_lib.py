@@ -19,7 +19,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must be imported before the library; see above)
 
 LIBRARY = Path(__file__).resolve().with_name("libasrattn.so")
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 # enum asrattn_status / asrattn_dtype / asrattn_causal
 OK = 0
@@ -103,6 +103,7 @@ class DecodeParams(ctypes.Structure):
         ("num_splits", _i32),
         ("dtype", _i32),
         ("scale", ctypes.c_float),
+        ("window", _i32),
     ]
 
 

@@ -356,6 +356,7 @@ def _decode_params(
     positions: Tensor | None,
     num_splits: int,
     scale: float | None,
+    window: int = 0,
 ) -> _lib.DecodeParams:
     params = _lib.DecodeParams()
     params.q, params.k, params.v, params.out = q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr()
@@ -373,6 +374,7 @@ def _decode_params(
     params.num_splits = num_splits
     params.dtype = _dtype_code(q, k, v)
     params.scale = 1.0 / math.sqrt(q.shape[2]) if scale is None else scale
+    params.window = 0 if window is None else window
     return params
 
 
@@ -388,9 +390,11 @@ def decode(
     out: Tensor | None = None,
     workspace: Tensor | None = None,
     pages: PageTable | None = None,
+    window: int | None = None,
 ) -> Tensor:
     """One query per sequence over a cache (``asrattn_decode``, or
-    ``asrattn_decode_paged`` with ``pages``).
+    ``asrattn_decode_paged`` with ``pages``).  ``window``: only the last
+    ``window`` of each row's keys (sliding-window attention).
 
     ``q`` ``(batch, heads_q, head_dim)``; ``k``/``v`` ``(batch, length,
     heads_kv, head_dim)``, any strides with a unit last one (pass
@@ -426,7 +430,7 @@ def decode(
         if lengths is not None and lengths.shape != (q.shape[0],):
             raise ValueError(f"key counts must have shape ({q.shape[0]},), got {tuple(lengths.shape)}")
     device = _check_device(q, k, v, out, seqused_k, positions, None if pages is None else pages.block_table)
-    params = _decode_params(q, k, v, out, seqused_k, positions, num_splits, scale)
+    params = _decode_params(q, k, v, out, seqused_k, positions, num_splits, scale, window)
     pk = None
     if pages is not None:
         pk, params.max_len_k = _paged(pages, k, v, q.shape[0])
@@ -467,6 +471,7 @@ def decode_append(
     out: Tensor | None = None,
     workspace: Tensor | None = None,
     pages: PageTable | None = None,
+    window: int | None = None,
 ) -> Tensor:
     """A decoder step with its prologue fused in (``asrattn_decode_append``;
     with ``pages``, ``k``/``v`` are page pools as for :func:`decode`):
@@ -519,7 +524,7 @@ def decode_append(
     positions = positions.contiguous()
     device = _check_device(q, k, v, out, positions, k_new, v_new, *extras,
                            None if pages is None else pages.block_table)
-    params = _decode_params(q, k, v, out, None, positions, num_splits, scale)
+    params = _decode_params(q, k, v, out, None, positions, num_splits, scale, window)
     pk = None
     if pages is not None:
         pk, params.max_len_k = _paged(pages, k, v, batch)

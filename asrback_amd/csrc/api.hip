@@ -79,13 +79,14 @@ int check_decode(const asrattn_decode_params* p) {
   if (rc != ASRATTN_OK) return rc;
   if (p->batch < 0) return fail(ASRATTN_ERR_INVALID, "batch must be >= 0, got %d", p->batch);
   if (p->max_len_k < 0) return fail(ASRATTN_ERR_INVALID, "max_len_k must be >= 0, got %d", p->max_len_k);
+  if (p->window < 0) return fail(ASRATTN_ERR_INVALID, "window must be >= 0, got %d", p->window);
   if (p->num_splits < 0 || p->num_splits > 1024)
     return fail(ASRATTN_ERR_INVALID, "num_splits must be in [0, 1024], got %d", p->num_splits);
   const int group = p->heads_q / p->heads_kv;
   if (!asrattn::decode_supported(p->dtype, p->head_dim, group))
     return fail(ASRATTN_ERR_UNSUPPORTED,
                 "no decode kernel for head_dim %d with %d query heads per kv head (supported: head_dim "
-                "64/128, 1/2/4 heads per kv head)",
+                "64/128/256, and 512 in bf16; 1/2/4/8 heads per kv head)",
                 p->head_dim, group);
   return ASRATTN_OK;
 }

@@ -1,544 +1,16 @@
-// Decoder-step attention: one query per sequence over a key/value cache.
-//
-// The step is bound by HBM: every key and value of a sequence is read once
-// and used for one (or, with grouped-query attention, g) dot products.  The
-// kernel therefore streams K and V with 16-byte loads, keeps a second batch
-// of loads in flight while it consumes the first, and does all arithmetic in
-// registers:
-//
-//   * K and V are read once, with nontemporal loads (no L2 allocation).
-//   * A key row (head_dim elements) is covered by LPK lanes, 16 bytes each;
-//     a wave loads 64 / LPK key rows per instruction, so every load touches
-//     whole rows.  Each group of LPK lanes runs its own online softmax over
-//     the keys it reads (a "stream"); the g query heads sharing the kv head
-//     ride along on the same loads.
-//   * A workgroup of W waves covers one (sequence, kv head) -- or, for small
-//     batches, one of `splits` key ranges of it.  Its streams merge first
-//     inside each wave (butterfly shuffles) and then across waves in LDS.
-//     With enough (sequence, kv head) pairs to fill the GPU there is one
-//     split and the workgroup writes the output; otherwise each split writes
-//     an unnormalized partial (o, max, sum) and a small combine kernel folds
-//     them.  No workgroup waits on another.
-//   * Sequence lengths are read from device memory (seqused_k or
-//     positions + 1), and splits past a sequence's end write an empty
-//     partial, so the grid depends only on shapes and the launch can be
-//     replayed from a graph while lengths change.
-//
-// Softmax runs in base 2: each reduced score q . k is multiplied by
-// scale * log2(e), so p = 2^(s - max) on v_exp_f32.
-//
-// Paged caches (asrattn_decode_paged): a load batch is U slices of NS
-// consecutive keys (one key per stream), NS-aligned; with page sizes that
-// are multiples of NS each slice lies in one page, whose pool index is one
-// uniform (scalar) load from the block table.  The slice's buffer resource
-// starts at that page and ends at the sequence's last key in it, so unused
-// page slots and pages past the sequence are never read.
-#include "common.hpp"
+// Decoder-step attention: kernel choice and launch (the kernels live in
+// decode_kernels.hpp, instantiated per element type in decode_bf16.hip and
+// decode_f32.hip).
+#include "decode_args.hpp"
 #include "kernels.hpp"
 
 namespace asrattn {
-namespace {
-
-struct DecodeArgs {
-  asrattn_decode_params p;
-  asrattn_append_params ap;  // the fused prologue (append variant only)
-  asrattn_paged_kv pk;       // the page table (paged variant only)
-  int page_shift;            // log2(pk.page_size)
-  float* ws_o;   // [batch][heads_q][splits][head_dim]
-  float* ws_ml;  // [batch][heads_q][splits][2]
-  int splits;
-  float c;  // scale * log2(e)
-};
-
-template <typename T, int HD, int G, int W>
-struct DecodeShape {
-  static constexpr int kEPL = Elem<T>::kPerVec;   // elements per lane per load
-  static constexpr int kLPK = HD / kEPL;          // lanes per key row
-  static constexpr int kKPW = 64 / kLPK;          // key rows per wave load (streams per wave)
-  static constexpr int kThreads = 64 * W;
-  static constexpr int kStreams = W * kKPW;       // softmax streams per workgroup
-  // Keys per stream per load batch; with four query heads per kv head the
-  // batches are halved so that two of them fit beside the heads' state in
-  // 128 VGPRs.
-  static constexpr int kUnroll = G >= 4 ? 2 : 4;
-  static constexpr int kStep = kStreams * kUnroll;  // keys per load batch
-  static_assert(kLPK >= 1 && kLPK <= 64 && (64 % kLPK) == 0, "head_dim/lane mapping");
-};
-
-// q . k over one lane's 16-byte slices, accumulated in fp32.
-template <typename T>
-__device__ __forceinline__ float dot16(const uint4& q, const uint4& k);
-
-template <>
-__device__ __forceinline__ float dot16<float>(const uint4& q, const uint4& k) {
-  float acc = __uint_as_float(q.x) * __uint_as_float(k.x);
-  acc = fmaf(__uint_as_float(q.y), __uint_as_float(k.y), acc);
-  acc = fmaf(__uint_as_float(q.z), __uint_as_float(k.z), acc);
-  return fmaf(__uint_as_float(q.w), __uint_as_float(k.w), acc);
-}
-
-// bf16 pairs on v_dot2c_f32_bf16: the products of two bf16 values are exact
-// in fp32, so this equals the unpacked fp32 dot product up to summation
-// order.
-template <>
-__device__ __forceinline__ float dot16<bf16_raw>(const uint4& q, const uint4& k) {
-  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-  auto pair = [](uint32_t x) { return __builtin_bit_cast(bf16x2_t, x); };
-  float acc = __builtin_amdgcn_fdot2_f32_bf16(pair(q.x), pair(k.x), 0.f, false);
-  acc = __builtin_amdgcn_fdot2_f32_bf16(pair(q.y), pair(k.y), acc, false);
-  acc = __builtin_amdgcn_fdot2_f32_bf16(pair(q.z), pair(k.z), acc, false);
-  return __builtin_amdgcn_fdot2_f32_bf16(pair(q.w), pair(k.w), acc, false);
-}
-
-template <typename T>
-__device__ __forceinline__ void unpack(const uint4& r, float* out);
-
-template <>
-__device__ __forceinline__ void unpack<float>(const uint4& r, float* out) {
-  out[0] = __uint_as_float(r.x); out[1] = __uint_as_float(r.y);
-  out[2] = __uint_as_float(r.z); out[3] = __uint_as_float(r.w);
-}
-
-template <>
-__device__ __forceinline__ void unpack<bf16_raw>(const uint4& r, float* out) {
-  out[0] = bf16_lo(r.x); out[1] = bf16_hi(r.x);
-  out[2] = bf16_lo(r.y); out[3] = bf16_hi(r.y);
-  out[4] = bf16_lo(r.z); out[5] = bf16_hi(r.z);
-  out[6] = bf16_lo(r.w); out[7] = bf16_hi(r.w);
-}
-
-template <typename T>
-__device__ __forceinline__ uint4 pack(const float* x);
-
-template <>
-__device__ __forceinline__ uint4 pack<float>(const float* x) {
-  return make_uint4(__float_as_uint(x[0]), __float_as_uint(x[1]), __float_as_uint(x[2]), __float_as_uint(x[3]));
-}
-
-template <>
-__device__ __forceinline__ uint4 pack<bf16_raw>(const float* x) {
-  return make_uint4(pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3]), pack_bf16x2(x[4], x[5]), pack_bf16x2(x[6], x[7]));
-}
-
-// x rounded to T (and back): where the reference's element-wise ops round.
-template <typename T>
-__device__ __forceinline__ float round_to(float x) {
-  if constexpr (sizeof(T) == 2) return bf16_to_f32(f32_to_bf16(x));
-  return x;
-}
-
-// Per-head RMSNorm and rotary embedding of one row slice -- lane `sub` of
-// the LPK lanes holding a head_dim row, EPL elements -- in the reference's
-// rounding order (qwen3_asr.py:322-330): the norm x * rsqrt(mean(x^2) +
-// eps) * w in fp32, rounded once; the rotation x c + r s with r = (-x[d/2:],
-// x[:d/2]) rounded after each product and after the sum.  Element e of lane
-// sub pairs with element e of lane sub ^ LPK/2.  w, cs and sn are the
-// lane's slices of the weights and tables (loaded by the caller); has_norm
-// and has_rot are uniform over the grid.  All lanes of the wave must take
-// part.
-template <typename T, int HD, int LPK>
-__device__ __forceinline__ uint4 norm_rotate(uint4 raw, bool has_norm, const uint4& w, bool has_rot, const uint4& cs,
-                                             const uint4& sn, float eps, int sub) {
-  constexpr int EPL = Elem<T>::kPerVec;
-  float x[EPL];
-  unpack<T>(raw, x);
-  if (has_norm) {
-    float ss = 0.f;
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) ss = fmaf(x[e], x[e], ss);
-    ss = group_sum<LPK>(ss);
-    const float r = rsqrtf(ss * (1.f / HD) + eps);
-    float wv[EPL];
-    unpack<T>(w, wv);
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) x[e] = round_to<T>(x[e] * r * wv[e]);
-  }
-  if (has_rot) {
-    float cv[EPL], sv[EPL];
-    unpack<T>(cs, cv);
-    unpack<T>(sn, sv);
-    const bool lower = sub < LPK / 2;
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) {
-      const float partner = __shfl_xor(x[e], LPK / 2, 64);
-      const float rot = lower ? -partner : partner;
-      x[e] = round_to<T>(round_to<T>(x[e] * cv[e]) + round_to<T>(rot * sv[e]));
-    }
-  }
-  return pack<T>(x);
-}
-
-// Online-softmax state of one stream for the G query heads of a kv head.
-template <typename T, int HD, int G, int W>
-struct Stream {
-  using S = DecodeShape<T, HD, G, W>;
-  static constexpr int EPL = S::kEPL;
-  uint4 q[G];   // the lane's raw 16-byte slice of each query head
-  float c;      // scale * log2(e), applied to the reduced score
-  float m[G], l[G], o[G][EPL];
-
-  // Starts the state from one key (k, v) when `mine`; the dot products run
-  // on every lane (their reductions need the whole wave).
-  __device__ __forceinline__ void seed(const uint4& k, const uint4& v, bool mine) {
-    float vf[EPL];
-    unpack<T>(v, vf);
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float s = group_sum<S::kLPK>(dot16<T>(q[g], k)) * c;
-      if (mine) {
-        m[g] = s;
-        l[g] = 1.f;
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) o[g][e] = vf[e];
-      }
-    }
-  }
-
-  __device__ __forceinline__ void init() {
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      m[g] = kNegInf;
-      l[g] = 0.f;
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) o[g][e] = 0.f;
-    }
-  }
-
-  // Folds one load batch (raw 16-byte lane slices of K and V); key u is
-  // valid when bit u of valid_mask is set.
-  __device__ __forceinline__ void consume(const uint4* kr, const uint4* vr, unsigned valid_mask) {
-    constexpr int U = S::kUnroll;
-    float s[U][G];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const float acc = group_sum<S::kLPK>(dot16<T>(q[g], kr[u]));
-        s[u][g] = (valid_mask >> u) & 1u ? acc * c : kNegInf;
-      }
-    }
-    float mu[G];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float mt = s[0][g];
-#pragma unroll
-      for (int u = 1; u < U; ++u) mt = fmaxf(mt, s[u][g]);
-      const float mn = fmaxf(m[g], mt);
-      mu[g] = mn == kNegInf ? 0.f : mn;
-      const float alpha = fast_exp2(m[g] - mu[g]);
-      l[g] *= alpha;
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) o[g][e] *= alpha;
-      m[g] = mn;
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      float vf[EPL];
-      unpack<T>(vr[u], vf);
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const float pu = fast_exp2(s[u][g] - mu[g]);
-        l[g] += pu;
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) o[g][e] = fmaf(pu, vf[e], o[g][e]);
-      }
-    }
-  }
-
-  // Merges the wave's streams (lane groups LPK apart) with butterfly
-  // shuffles; afterwards every group holds the wave's state.
-  __device__ __forceinline__ void merge_wave() {
-#pragma unroll
-    for (int off = S::kLPK; off < 64; off <<= 1) {
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const float m2 = __shfl_xor(m[g], off, 64);
-        const float l2 = __shfl_xor(l[g], off, 64);
-        const float mn = fmaxf(m[g], m2);
-        const float mu = mn == kNegInf ? 0.f : mn;
-        const float w1 = fast_exp2(m[g] - mu);
-        const float w2 = fast_exp2(m2 - mu);
-        l[g] = l[g] * w1 + l2 * w2;
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) o[g][e] = o[g][e] * w1 + __shfl_xor(o[g][e], off, 64) * w2;
-        m[g] = mn;
-      }
-    }
-  }
-};
-
-// At most 128 VGPRs, so that four waves fit per SIMD (two 8-wave workgroups
-// per CU).
-//
-// APPEND: the fused prologue of asrattn_decode_append.  q and the step's key
-// are normalized and rotated in registers; the cache supplies keys
-// 0 .. positions[b] - 1 and the new key/value join from registers (the last
-// split folds them into its state); the first split writes them to the
-// cache at positions[b].  No workgroup reads that slot, so splits need no
-// ordering among themselves.
-template <typename T, int HD, int G, int W, bool APPEND, bool PAGED>
-__global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeArgs a) {
-  using S = DecodeShape<T, HD, G, W>;
-  constexpr int EPL = S::kEPL, LPK = S::kLPK, NS = S::kStreams, U = S::kUnroll, STEP = S::kStep;
-  const asrattn_decode_params& p = a.p;
-
-  const int split = blockIdx.x;
-  const int hkv = blockIdx.y;
-  const int b = blockIdx.z;
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int sub = lane % LPK;
-  const int stream = wave * S::kKPW + lane / LPK;
-
-  const int64_t pos = APPEND ? p.positions[b] : 0;
-  const int n = APPEND ? (int)min(max(pos, (int64_t)0), (int64_t)p.max_len_k)
-                       : decode_key_count(p.seqused_k, p.positions, b, p.max_len_k);
-  int chunk = (n + a.splits - 1) / a.splits;
-  if constexpr (PAGED) chunk = (chunk + NS - 1) / NS * NS;  // slices stay inside pages
-  const int k0 = min(n, split * chunk);
-  const int k1 = min(n, k0 + chunk);
-
-  // q is used raw (no unpacking), so its load latency overlaps the first
-  // K/V batch's.
-  Stream<T, HD, G, W> st;
-  {
-    const T* qp = static_cast<const T*>(p.q) + (int64_t)b * p.q_batch_stride +
-                  (int64_t)hkv * G * p.q_head_stride + sub * EPL;
-#pragma unroll
-    for (int g = 0; g < G; ++g) st.q[g] = *reinterpret_cast<const uint4*>(qp + (int64_t)g * p.q_head_stride);
-  }
-  st.c = a.c;
-  st.init();
-  // The prologue's inputs load here, before the first K/V batch; its
-  // arithmetic runs after that batch is issued.
-  const asrattn_append_params& ap = a.ap;
-  const bool has_norm = APPEND && ap.q_norm != nullptr;
-  const bool has_rot = APPEND && ap.cos != nullptr;
-  uint4 knew = {}, vnew = {}, qw = {}, kw = {}, cs = {}, sn = {};
-  if constexpr (APPEND) {
-    const T* knp = static_cast<const T*>(ap.k_new) + (int64_t)b * ap.kn_batch_stride + (int64_t)hkv * ap.kn_head_stride;
-    const T* vnp = static_cast<const T*>(ap.v_new) + (int64_t)b * ap.vn_batch_stride + (int64_t)hkv * ap.vn_head_stride;
-    // Absent weights or tables read k_new's slice instead (and are unused):
-    // the loads stay unconditional, so no branch joins their registers and
-    // forces a wait before the first K/V batch.
-    const T* qwp = has_norm ? static_cast<const T*>(ap.q_norm) : knp;
-    const T* kwp = has_norm ? static_cast<const T*>(ap.k_norm) : knp;
-    const T* csp = has_rot ? static_cast<const T*>(ap.cos) + (int64_t)b * ap.rope_batch_stride : knp;
-    const T* snp = has_rot ? static_cast<const T*>(ap.sin) + (int64_t)b * ap.rope_batch_stride : knp;
-    knew = *reinterpret_cast<const uint4*>(knp + sub * EPL);
-    vnew = *reinterpret_cast<const uint4*>(vnp + sub * EPL);
-    qw = *reinterpret_cast<const uint4*>(qwp + sub * EPL);
-    kw = *reinterpret_cast<const uint4*>(kwp + sub * EPL);
-    cs = *reinterpret_cast<const uint4*>(csp + sub * EPL);
-    sn = *reinterpret_cast<const uint4*>(snp + sub * EPL);
-  }
-
-  // K and V of this (sequence, kv head) through buffer resources that end
-  // at the split's last key: loads past it return zeros without a branch,
-  // so the two load batches stay in flight across the loop.
-  // (Paged: the pool, past the sequence's first page.)
-  const int64_t kbatch = PAGED ? 0 : (int64_t)b * p.k_batch_stride;
-  const int64_t vbatch = PAGED ? 0 : (int64_t)b * p.v_batch_stride;
-  const char* kbase =
-      reinterpret_cast<const char*>(static_cast<const T*>(p.k) + kbatch + (int64_t)hkv * p.k_head_stride);
-  const char* vbase =
-      reinterpret_cast<const char*>(static_cast<const T*>(p.v) + vbatch + (int64_t)hkv * p.v_head_stride);
-  const uint32_t kts = (uint32_t)(p.k_token_stride * (int64_t)sizeof(T));
-  const uint32_t vts = (uint32_t)(p.v_token_stride * (int64_t)sizeof(T));
-  const __amdgpu_buffer_rsrc_t krs = buffer_rsrc(kbase, (uint32_t)k1 * kts);
-  const __amdgpu_buffer_rsrc_t vrs = buffer_rsrc(vbase, (uint32_t)k1 * vts);
-  const uint32_t lane_bytes = sub * EPL * (uint32_t)sizeof(T);
-
-  // Paged: pool page of logical page pi of this sequence, or -1 when the
-  // entry is missing or outside the pool (its keys are skipped).
-  const int32_t* bt = PAGED ? a.pk.block_table + (int64_t)b * a.pk.bt_stride : nullptr;
-  auto pool_page = [&](int pi) -> int {
-    if (pi >= a.pk.bt_stride) return -1;
-    const int e = bt[__builtin_amdgcn_readfirstlane(pi)];
-    return e >= 0 && e < a.pk.num_pages ? e : -1;
-  };
-
-  // Key u of the batch starting at `base` is base + u * NS + stream.
-  auto load = [&](uint4* kr, uint4* vr, int base) -> unsigned {
-    unsigned mask = 0;
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int j = base + u * NS + stream;
-      if constexpr (PAGED) {
-        const int j0 = base + u * NS;  // uniform; the slice lies in one page
-        const int pi = j0 >> a.page_shift;
-        const int first = pi << a.page_shift;
-        const int page = pool_page(pi);
-        const uint32_t keys = page >= 0 ? (uint32_t)min(max(k1 - first, 0), a.pk.page_size) : 0u;
-        const int64_t pg = page >= 0 ? page : 0;
-        const __amdgpu_buffer_rsrc_t kp = buffer_rsrc(kbase + pg * a.pk.k_page_stride * (int64_t)sizeof(T), keys * kts);
-        const __amdgpu_buffer_rsrc_t vp = buffer_rsrc(vbase + pg * a.pk.v_page_stride * (int64_t)sizeof(T), keys * vts);
-        kr[u] = buffer_load16_stream(kp, (uint32_t)(j - first) * kts + lane_bytes);
-        vr[u] = buffer_load16_stream(vp, (uint32_t)(j - first) * vts + lane_bytes);
-        mask |= (j < k1 && page >= 0 ? 1u : 0u) << u;
-      } else {
-        kr[u] = buffer_load16_stream(krs, (uint32_t)j * kts + lane_bytes);
-        vr[u] = buffer_load16_stream(vrs, (uint32_t)j * vts + lane_bytes);
-        mask |= (j < k1 ? 1u : 0u) << u;
-      }
-    }
-    return mask;
-  };
-
-  // Two register batches in ping-pong: the next batch is in flight while the
-  // current one is consumed.
-  // The first batch is issued unconditionally: with k0 >= k1 its offsets all
-  // lie past the resource's end and read zeros.
-  uint4 ka[U], va[U], kb[U], vb[U];
-  unsigned mb = 0;
-  unsigned ma = load(ka, va, k0);
-  if constexpr (APPEND) {
-    __builtin_amdgcn_sched_barrier(0);  // keep the prologue below the batch's issue
-#pragma unroll
-    for (int g = 0; g < G; ++g) st.q[g] = norm_rotate<T, HD, LPK>(st.q[g], has_norm, qw, has_rot, cs, sn, ap.eps, sub);
-    knew = norm_rotate<T, HD, LPK>(knew, has_norm, kw, has_rot, cs, sn, ap.eps, sub);
-    st.seed(knew, vnew, split == a.splits - 1 && stream == 0);
-  }
-  for (int base = k0; base < k1; base += 2 * STEP) {
-    mb = load(kb, vb, base + STEP);
-    st.consume(ka, va, ma);
-    if (base + STEP >= k1) break;
-    ma = load(ka, va, base + 2 * STEP);
-    st.consume(kb, vb, mb);
-  }
-
-  if constexpr (APPEND) {
-    if (split == 0 && stream == 0 && pos >= 0 && pos < p.max_len_k) {
-      int64_t koff = pos * kts, voff = pos * vts;
-      bool write = true;
-      if constexpr (PAGED) {
-        const int pi = (int)(pos >> a.page_shift);
-        const int page = pool_page(pi);
-        const int64_t slot = pos - ((int64_t)pi << a.page_shift);
-        write = page >= 0;
-        koff = (int64_t)page * a.pk.k_page_stride * (int64_t)sizeof(T) + slot * kts;
-        voff = (int64_t)page * a.pk.v_page_stride * (int64_t)sizeof(T) + slot * vts;
-      }
-      if (write) {
-        *reinterpret_cast<uint4*>(const_cast<char*>(kbase) + koff + lane_bytes) = knew;
-        *reinterpret_cast<uint4*>(const_cast<char*>(vbase) + voff + lane_bytes) = vnew;
-      }
-    }
-  }
-
-  st.merge_wave();
-
-  // Merge the waves in LDS.
-  __shared__ float sm_m[W][G];
-  __shared__ float sm_l[W][G];
-  __shared__ float sm_o[W][G][HD];
-  if (lane < LPK) {
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      if (lane == 0) {
-        sm_m[wave][g] = st.m[g];
-        sm_l[wave][g] = st.l[g];
-      }
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) sm_o[wave][g][sub * EPL + e] = st.o[g][e];
-    }
-  }
-  __syncthreads();
-
-  for (int t = threadIdx.x; t < G * HD; t += S::kThreads) {
-    const int g = t / HD;
-    const int d = t % HD;
-    float mx = kNegInf;
-#pragma unroll
-    for (int w = 0; w < W; ++w) mx = fmaxf(mx, sm_m[w][g]);
-    const float mxu = mx == kNegInf ? 0.f : mx;
-    float lsum = 0.f, osum = 0.f;
-#pragma unroll
-    for (int w = 0; w < W; ++w) {
-      const float wt = fast_exp2(sm_m[w][g] - mxu);
-      lsum = fmaf(sm_l[w][g], wt, lsum);
-      osum = fmaf(sm_o[w][g][d], wt, osum);
-    }
-    const int hq = hkv * G + g;
-    if (a.splits == 1) {
-      T* op = static_cast<T*>(p.out) + (int64_t)b * p.o_batch_stride + (int64_t)hq * p.o_head_stride + d;
-      Elem<T>::store1(op, lsum > 0.f ? osum / lsum : 0.f);
-    } else {
-      const int64_t idx = ((int64_t)b * p.heads_q + hq) * a.splits + split;
-      a.ws_o[idx * HD + d] = osum;
-      if (d == 0) {
-        a.ws_ml[idx * 2] = mx;
-        a.ws_ml[idx * 2 + 1] = lsum;
-      }
-    }
-  }
-}
-
-// Folds the splits' partials of one (sequence, query head) into the output.
-template <typename T, int HD>
-__global__ __launch_bounds__(HD) void decode_combine_kernel(const DecodeArgs a) {
-  const asrattn_decode_params& p = a.p;
-  const int hq = blockIdx.x;
-  const int b = blockIdx.y;
-  const int d = threadIdx.x;
-  const int64_t idx0 = ((int64_t)b * p.heads_q + hq) * a.splits;
-  float mx = kNegInf;
-  for (int s = 0; s < a.splits; ++s) mx = fmaxf(mx, a.ws_ml[(idx0 + s) * 2]);
-  const float mxu = mx == kNegInf ? 0.f : mx;
-  float lsum = 0.f, osum = 0.f;
-  for (int s = 0; s < a.splits; ++s) {
-    const float w = fast_exp2(a.ws_ml[(idx0 + s) * 2] - mxu);
-    lsum = fmaf(a.ws_ml[(idx0 + s) * 2 + 1], w, lsum);
-    osum = fmaf(a.ws_o[(idx0 + s) * HD + d], w, osum);
-  }
-  T* op = static_cast<T*>(p.out) + (int64_t)b * p.o_batch_stride + (int64_t)hq * p.o_head_stride + d;
-  Elem<T>::store1(op, lsum > 0.f ? osum / lsum : 0.f);
-}
-
-template <typename T, int HD, int G, int W>
-hipError_t launch_typed(const DecodeArgs& a, bool append, hipStream_t stream) {
-  const asrattn_decode_params& p = a.p;
-  dim3 grid(a.splits, p.heads_kv, p.batch);
-  const bool paged = a.pk.block_table != nullptr;
-  if (append && paged)
-    hipLaunchKernelGGL((decode_kernel<T, HD, G, W, true, true>), grid, dim3(64 * W), 0, stream, a);
-  else if (append)
-    hipLaunchKernelGGL((decode_kernel<T, HD, G, W, true, false>), grid, dim3(64 * W), 0, stream, a);
-  else if (paged)
-    hipLaunchKernelGGL((decode_kernel<T, HD, G, W, false, true>), grid, dim3(64 * W), 0, stream, a);
-  else
-    hipLaunchKernelGGL((decode_kernel<T, HD, G, W, false, false>), grid, dim3(64 * W), 0, stream, a);
-  hipError_t err = hipGetLastError();
-  if (err != hipSuccess || a.splits == 1) return err;
-  hipLaunchKernelGGL((decode_combine_kernel<T, HD>), dim3(p.heads_q, p.batch), dim3(HD), 0, stream, a);
-  return hipGetLastError();
-}
-
-template <typename T, int HD, int G>
-hipError_t launch_waves(const DecodeArgs& a, int waves, bool append, hipStream_t stream) {
-  switch (waves) {
-    case 4: return launch_typed<T, HD, G, 4>(a, append, stream);
-    case 8: return launch_typed<T, HD, G, 8>(a, append, stream);
-    default: return launch_typed<T, HD, G, 16>(a, append, stream);
-  }
-}
-
-template <typename T, int HD>
-hipError_t launch_hd(const DecodeArgs& a, int group, int waves, bool append, hipStream_t stream) {
-  switch (group) {
-    case 1: return launch_waves<T, HD, 1>(a, waves, append, stream);
-    case 2: return launch_waves<T, HD, 2>(a, waves, append, stream);
-    case 4: return launch_waves<T, HD, 4>(a, waves, append, stream);
-    default: return hipErrorInvalidValue;
-  }
-}
-
-}  // namespace
 
 bool decode_supported(int dtype, int head_dim, int group) {
   const bool dt = dtype == ASRATTN_F32 || dtype == ASRATTN_BF16;
-  const bool hd = head_dim == 64 || head_dim == 128;
-  const bool g = group == 1 || group == 2 || group == 4;
+  // A key row is read by at most one wave: 64 lanes x 16 bytes.
+  const bool hd = head_dim == 64 || head_dim == 128 || head_dim == 256 || (head_dim == 512 && dtype == ASRATTN_BF16);
+  const bool g = group == 1 || group == 2 || group == 4 || group == 8;
   return dt && hd && g;
 }
 
@@ -575,12 +47,8 @@ hipError_t launch_decode(const asrattn_decode_params& p, const asrattn_append_pa
   a.c = p.scale * kLog2e;
   const int group = p.heads_q / p.heads_kv;
   const int waves = decode_waves(p, splits, paged != nullptr ? paged->page_size : 0);
-  if (p.dtype == ASRATTN_BF16) {
-    return p.head_dim == 64 ? launch_hd<bf16_raw, 64>(a, group, waves, app, stream)
-                            : launch_hd<bf16_raw, 128>(a, group, waves, app, stream);
-  }
-  return p.head_dim == 64 ? launch_hd<float, 64>(a, group, waves, app, stream)
-                          : launch_hd<float, 128>(a, group, waves, app, stream);
+  return p.dtype == ASRATTN_BF16 ? launch_decode_bf16(a, p.head_dim, group, waves, app, stream)
+                                 : launch_decode_f32(a, p.head_dim, group, waves, app, stream);
 }
 
 }  // namespace asrattn

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define ASRATTN_ABI_VERSION 4
+#define ASRATTN_ABI_VERSION 5
 
 enum asrattn_status {
   ASRATTN_OK = 0,
@@ -150,7 +150,8 @@ int asrattn_fwd_fsmn(const asrattn_fwd_params* params, const asrattn_fsmn_params
  * workgroups (split-K) and a second kernel merges their partials.
  *
  *   out[b, h, :] = softmax_j(scale * q[b, h, :] . k[b, j, h / g, :]) v[b, j, h / g, :]
- *   for j < n_b,  n_b = min(max_len_k, seqused_k[b])      (seqused_k given)
+ *   for n_b - window <= j < n_b (window > 0) or j < n_b (window == 0),
+ *                 n_b = min(max_len_k, seqused_k[b])      (seqused_k given)
  *                 n_b = min(max_len_k, positions[b] + 1)  (positions given)
  *                 n_b = max_len_k                         (neither)
  *
@@ -194,6 +195,8 @@ typedef struct asrattn_decode_params {
   int32_t num_splits; /* 0: chosen from batch, heads and max_len_k */
   int32_t dtype;
   float scale;
+  int32_t window; /* > 0: each query sees only its last `window` keys (sliding-window
+                     attention, gemma4.py:720-725); 0: all n_b */
 } asrattn_decode_params;
 
 /* Bytes of workspace asrattn_decode needs for these parameters (pointers are

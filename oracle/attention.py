@@ -22,12 +22,14 @@ def sdpa(
     attn_mask: Tensor | None = None,
     is_causal: bool = False,
     enable_gqa: bool = False,
+    scale: float | None = None,
 ) -> Tensor:
     """``F.scaled_dot_product_attention`` on ``(B, H, L, D)`` tensors, as called
-    at ``whisper.py:102-104``, ``sensevoice.py:128-133`` and
-    ``qwen3_asr.py:176-180``/``:429-431``."""
+    at ``whisper.py:102-104``, ``sensevoice.py:128-133``,
+    ``qwen3_asr.py:176-180``/``:429-431`` and (``scale=1.0``)
+    ``gemma4.py:552-559``/``:580-586``."""
     return F.scaled_dot_product_attention(
-        query, key, value, attn_mask=attn_mask, is_causal=is_causal, enable_gqa=enable_gqa
+        query, key, value, attn_mask=attn_mask, is_causal=is_causal, enable_gqa=enable_gqa, scale=scale
     )
 
 
@@ -44,6 +46,28 @@ def whisper_step_mask(positions: Tensor, length: int) -> Tensor:
     (``whisper.py:263-264``).  Shape ``(B, 1, 1, length)``."""
     key_positions = torch.arange(length, device=positions.device)
     return (key_positions[None, :] <= positions[:, None])[:, None, None, :]
+
+
+def gemma_step_mask(positions: Tensor, length: int, window: int | None) -> Tensor:
+    """Mask of a Gemma 4 decoder step (``gemma4.py:717-725``): key ``j``
+    visible to row ``b`` iff ``j <= positions[b]`` and, on sliding-window
+    layers, ``j > positions[b] - window``.  Shape ``(B, 1, 1, length)``."""
+    key_positions = torch.arange(length, device=positions.device)[None, :]
+    mask = key_positions <= positions[:, None]
+    if window is not None:
+        mask = mask & (key_positions > positions[:, None] - window)
+    return mask[:, None, None, :]
+
+
+def gemma_prefill_mask(sizes: Tensor, longest: int, window: int | None) -> Tensor:
+    """Mask of the Gemma 4 padded prompt pass (``gemma4.py:1227-1235``):
+    causal, keys before each prompt's size, and on sliding-window layers
+    keys within ``window`` of the query.  Shape ``(B, 1, longest, longest)``."""
+    positions = torch.arange(longest, device=sizes.device)
+    causal = (positions[None, :] <= positions[:, None]) & (positions[None, None, :] < sizes[:, None, None])
+    if window is not None:
+        causal = causal & (positions[None, :] > positions[:, None] - window)
+    return causal[:, None]
 
 
 def key_padding_mask(lengths: Tensor, length: int) -> Tensor:

@@ -502,6 +502,74 @@ def test_paged_decode_append_matches_slab(ops, device, dtype):
         assert bool(((after == before) | (before.isnan() & after.isnan())).all())
 
 
+@pytest.mark.parametrize(
+    "dtype,hd,heads_q,heads_kv,window,page,splits",
+    [
+        (torch.bfloat16, 256, 8, 1, 512, 0, 0),
+        (torch.bfloat16, 512, 8, 1, 0, 0, 0),
+        (torch.bfloat16, 512, 8, 2, 0, 0, 3),
+        (torch.bfloat16, 256, 8, 2, 512, 64, 0),
+        (torch.bfloat16, 256, 8, 1, 512, 16, 5),
+        (torch.float32, 256, 8, 1, 512, 0, 0),
+        (torch.float32, 256, 8, 2, 100, 0, 4),
+        (torch.bfloat16, 128, 16, 8, 300, 0, 0),
+    ],
+)
+def test_gemma_decode_window_and_head_sizes(ops, device, dtype, hd, heads_q, heads_kv, window, page, splits):
+    """Gemma 4 text steps (gemma4.py:563-587, masks :717-725): head_dim 256
+    (sliding layers, 512-key window) and 512 (full layers), 8 query heads
+    over 1 or 2 kv heads, scale 1.0, against the oracle's masked SDPA;
+    lengths around the window and the 1280-position cache end, slab and
+    paged caches, split keys."""
+    say("gemma decode", dtype, hd, heads_q, heads_kv, window, page, splits)
+    batch, length = 7, 1280
+    lengths = np.array([1, 511, 512, 513, 1279, 1280, 700], dtype=np.int32)
+    q = randn(batch, heads_q, hd, seed=101, dtype=dtype) * 0.1
+    keys = randn(batch, length, heads_kv, hd, seed=102, dtype=dtype)
+    values = randn(batch, length, heads_kv, hd, seed=103, dtype=dtype)
+    positions = torch.from_numpy(lengths.astype(np.int64) - 1)
+    mask = oa.gemma_step_mask(positions, length, window or None)
+    grouped = q.float().view(batch, heads_kv, heads_q // heads_kv, hd)
+    ref = oa.sdpa(grouped, keys.float().transpose(1, 2), values.float().transpose(1, 2), attn_mask=mask, scale=1.0)
+    ref = ref.reshape(batch, heads_q, hd)
+    used = torch.from_numpy(lengths).to(device)
+    if page:
+        pool_k, pool_v, table = _paginate(keys, values, lengths, page, seed=104)
+        out = ops.decode(q.to(device), pool_k.to(device), pool_v.to(device), seqused_k=used, scale=1.0,
+                         window=window, num_splits=splits, pages=ops.PageTable(table.to(device), length))
+    else:
+        out = ops.decode(q.to(device), keys.to(device), values.to(device), seqused_k=used, scale=1.0,
+                         window=window, num_splits=splits)
+    assert torch.isfinite(out).all()
+    assert max_rel_err(out, ref) < TOL[dtype]
+
+
+def test_gemma_decode_append_window(ops, device):
+    """The appending step with a window: the new key is the last of the
+    window's keys, and only cache keys position - window + 1 .. position - 1
+    join it."""
+    say("gemma decode append, window")
+    batch, heads_q, heads_kv, hd, length, window = 6, 8, 1, 256, 1280, 512
+    positions = torch.tensor([0, 510, 511, 512, 1000, 1279])
+    q = randn(batch, heads_q, hd, seed=111, dtype=torch.bfloat16) * 0.1
+    k_new = randn(batch, heads_kv, hd, seed=112, dtype=torch.bfloat16)
+    v_new = randn(batch, heads_kv, hd, seed=113, dtype=torch.bfloat16)
+    keys = randn(batch, length, heads_kv, hd, seed=114, dtype=torch.bfloat16)
+    values = randn(batch, length, heads_kv, hd, seed=115, dtype=torch.bfloat16)
+    rows = torch.arange(batch)
+    ref_k, ref_v = keys.clone(), values.clone()
+    ref_k[rows, positions] = k_new
+    ref_v[rows, positions] = v_new
+    mask = oa.gemma_step_mask(positions, length, window)
+    grouped = q.float().view(batch, heads_kv, heads_q // heads_kv, hd)
+    ref = oa.sdpa(grouped, ref_k.float().transpose(1, 2), ref_v.float().transpose(1, 2), attn_mask=mask, scale=1.0)
+    kd, vd = keys.to(device), values.to(device)
+    out = ops.decode_append(q.to(device), k_new.to(device), v_new.to(device), kd, vd, positions.to(device),
+                            scale=1.0, window=window)
+    assert max_rel_err(out, ref.reshape(batch, heads_q, hd)) < TOL[torch.bfloat16]
+    assert torch.equal(kd.cpu()[rows, positions], k_new) and torch.equal(vd.cpu()[rows, positions], v_new)
+
+
 def test_decode_append_whisper_cache_without_norm(ops, device):
     """The Whisper step's scatter + attention (whisper.py:224-237) fused, no
     norm or rotation, into a (batch, heads, length, head_dim) cache through

@@ -133,6 +133,46 @@ def test_step_equals_last_row_of_causal_prefill():
         assert max_rel_err(step, full[:, :, p : p + 1]) < 1e-12
 
 
+def test_gemma_masks_match_explicit_loops():
+    """gemma4.py:717-725 (step) and :1227-1235 (prompt pass), restated as
+    loops over (row, query, key)."""
+    positions, length, window = torch.tensor([0, 3, 9, 15]), 16, 5
+    for w in (None, window):
+        step = oa.gemma_step_mask(positions, length, w)
+        for b, p in enumerate(positions.tolist()):
+            for j in range(length):
+                want = j <= p and (w is None or j > p - w)
+                assert bool(step[b, 0, 0, j]) == want
+    sizes, longest = torch.tensor([16, 7, 1]), 16
+    for w in (None, window):
+        mask = oa.gemma_prefill_mask(sizes, longest, w)
+        assert mask.shape == (3, 1, 16, 16)
+        for b, n in enumerate(sizes.tolist()):
+            for i in range(longest):
+                for j in range(longest):
+                    want = j <= i and j < n and (w is None or j > i - w)
+                    assert bool(mask[b, 0, i, j]) == want
+
+
+def test_gemma_window_step_equals_prefill_row_and_window_slice():
+    """Unscaled (scale=1.0) windowed attention: a step at position p equals
+    row p of the windowed prompt pass, and equals plain attention over the
+    keys p - w + 1 .. p alone."""
+    g = torch.Generator().manual_seed(12)
+    q, k, v = (torch.randn(1, 2, 20, 16, generator=g, dtype=torch.float64) * 0.3 for _ in range(3))
+    w = 6
+    full = oa.sdpa(q, k, v, attn_mask=oa.gemma_prefill_mask(torch.tensor([20]), 20, w), scale=1.0)
+    for p in (0, 4, 5, 6, 19):
+        step = oa.sdpa(q[:, :, p : p + 1], k, v, attn_mask=oa.gemma_step_mask(torch.tensor([p]), 20, w), scale=1.0)
+        assert max_rel_err(step, full[:, :, p : p + 1]) < 1e-12
+        lo = max(0, p - w + 1)
+        sliced = oa.sdpa(q[:, :, p : p + 1], k[:, :, lo : p + 1], v[:, :, lo : p + 1], scale=1.0)
+        assert max_rel_err(step, sliced) < 1e-12
+        # closed form, scale 1: per head, softmax of the raw dot products
+        weights = torch.einsum("hd,hjd->hj", q[0, :, p], k[0, :, lo : p + 1]).softmax(-1)
+        assert max_rel_err(step[0, :, 0], torch.einsum("hj,hjd->hd", weights, v[0, :, lo : p + 1])) < 1e-12
+
+
 def test_step_is_independent_of_cache_bucket():
     g = torch.Generator().manual_seed(4)
     q = torch.randn(3, 2, 1, 64, generator=g, dtype=torch.float64)
