@@ -19,7 +19,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must be imported before the library; see above)
 
 LIBRARY = Path(__file__).resolve().with_name("libasrattn.so")
-ABI_VERSION = 5
+ABI_VERSION = 7
 
 # enum asrattn_status / asrattn_dtype / asrattn_causal
 OK = 0
@@ -72,6 +72,7 @@ class FwdParams(ctypes.Structure):
         ("dtype", _i32),
         ("scale", ctypes.c_float),
         ("flags", _i32),
+        ("window", _i32),
     ]
 
 
@@ -152,6 +153,32 @@ class PagedKV(ctypes.Structure):
     ]
 
 
+class LocalParams(ctypes.Structure):
+    """``asrattn_local_params``."""
+
+    _fields_ = [
+        ("q", _ptr),
+        ("k", _ptr),
+        ("v", _ptr),
+        ("rel", _ptr),
+        ("out", _ptr),
+        *[(f"{t}_{axis}_stride", _i64) for t in ("q", "k", "v", "o") for axis in ("batch", "token", "head")],
+        ("rel_position_stride", _i64),
+        ("rel_head_stride", _i64),
+        ("lengths", _ptr),
+        ("batch", _i32),
+        ("tokens", _i32),
+        ("heads", _i32),
+        ("head_dim", _i32),
+        ("chunk", _i32),
+        ("past", _i32),
+        ("future", _i32),
+        ("rel_positions", _i32),
+        ("softcap", ctypes.c_float),
+        ("invalid", ctypes.c_float),
+    ]
+
+
 # Every symbol include/asrattn.h declares, with (restype, argtypes).
 SIGNATURES = {
     "asrattn_fwd": (ctypes.c_int, [ctypes.POINTER(FwdParams), _ptr]),
@@ -169,6 +196,7 @@ SIGNATURES = {
         [ctypes.POINTER(DecodeParams), ctypes.POINTER(AppendParams), ctypes.POINTER(PagedKV), _ptr,
          ctypes.c_size_t, _ptr],
     ),
+    "asrattn_local": (ctypes.c_int, [ctypes.POINTER(LocalParams), _ptr]),
     "asrattn_choose": (
         ctypes.c_int,
         [_ptr, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, _ptr, _ptr, _ptr, _ptr],

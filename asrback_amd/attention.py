@@ -187,6 +187,7 @@ def _fwd_params(
     seqused_k: Tensor | None,
     scale: float | None,
     force_valu: bool,
+    window: int = 0,
 ) -> tuple[_lib.FwdParams, Tensor, torch.device, tuple]:
     """``asrattn_fwd_params`` for :func:`flash`; returns them with ``out``,
     the device and the tensors the parameters point into (kept alive until
@@ -257,6 +258,7 @@ def _fwd_params(
     params.dtype = dtype
     params.scale = 1.0 / math.sqrt(head_dim) if scale is None else scale
     params.flags = _lib.FWD_FORCE_VALU if force_valu else 0
+    params.window = window or 0
     return params, out, device, (q, k, v, cu_seqlens_q, cu_seqlens_k, seqused_k)
 
 
@@ -274,8 +276,11 @@ def flash(
     seqused_k: Tensor | None = None,
     scale: float | None = None,
     force_valu: bool = False,
+    window: int | None = None,
 ) -> Tensor:
-    """Multi-row attention (``asrattn_fwd``).
+    """Multi-row attention (``asrattn_fwd``).  ``window`` (causal only):
+    each query also skips keys more than ``window - 1`` before its last
+    visible one (sliding-window attention).
 
     Padded layout: ``q`` ``(batch, len_q, heads_q, head_dim)``, ``k``/``v``
     ``(batch, len_k, heads_kv, head_dim)``; packed layout (``cu_seqlens_*``
@@ -283,7 +288,8 @@ def flash(
     (a new contiguous tensor unless ``out`` is given).
     """
     params, out, device, keep = _fwd_params(
-        q, k, v, out, causal, cu_seqlens_q, cu_seqlens_k, max_len_q, max_len_k, seqused_k, scale, force_valu
+        q, k, v, out, causal, cu_seqlens_q, cu_seqlens_k, max_len_q, max_len_k, seqused_k, scale, force_valu,
+        window or 0,
     )
     lib = _lib.load()
     _lib.check(lib.asrattn_fwd(ctypes.byref(params), _stream(device)), "asrattn_fwd")
@@ -554,6 +560,62 @@ def decode_append(
     return out
 
 
+def local_attention(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    rel: Tensor,
+    lengths: Tensor,
+    *,
+    chunk: int,
+    past: int,
+    future: int,
+    softcap: float,
+    invalid: float,
+    out: Tensor | None = None,
+) -> Tensor:
+    """Blocked local attention with relative position scores
+    (``asrattn_local``; Gemma 4's audio attention, ``gemma4.py:240-282``):
+    float32 ``q``/``k``/``v`` ``(batch, tokens, heads, head_dim)`` (already
+    scaled as the module scales them), ``rel`` ``(positions, heads,
+    head_dim)`` the relative keys of distances ``past .. 0``, ``lengths``
+    int32 valid tokens per sequence.  Returns float32 ``(batch, tokens,
+    heads, head_dim)``."""
+    for name, t in (("q", q), ("k", k), ("v", v), ("rel", rel)):
+        if t.dtype != torch.float32:
+            raise TypeError(f"local_attention computes in float32; {name} is {t.dtype}")
+        if t.stride(-1) != 1:
+            raise ValueError(f"{name} needs a unit last stride")
+    if q.dim() != 4 or k.shape != q.shape or v.shape != q.shape:
+        raise ValueError("q, k and v must share one (batch, tokens, heads, head_dim) shape")
+    batch, tokens, heads, head_dim = q.shape
+    if rel.dim() != 3 or rel.shape[1:] != (heads, head_dim):
+        raise ValueError(f"rel must be (positions, {heads}, {head_dim}), got {tuple(rel.shape)}")
+    lengths = _int32(lengths, "lengths")
+    if lengths.shape != (batch,):
+        raise ValueError(f"lengths must be ({batch},)")
+    if out is None:
+        out = torch.empty(q.shape, dtype=torch.float32, device=q.device)
+    elif out.shape != q.shape or out.dtype != torch.float32 or out.stride(-1) != 1:
+        raise ValueError("out must be a float32 tensor of q's shape with a unit last stride")
+    device = _check_device(q, k, v, rel, lengths, out)
+    if device.type != "cuda":
+        raise RuntimeError(f"attention kernels run on the GPU only; got tensors on {device}")
+    params = _lib.LocalParams()
+    params.q, params.k, params.v, params.rel, params.out = (t.data_ptr() for t in (q, k, v, rel, out))
+    for prefix, t in (("q", q), ("k", k), ("v", v), ("o", out)):
+        for axis, stride in zip(("batch", "token", "head"), t.stride()[:3]):
+            setattr(params, f"{prefix}_{axis}_stride", stride)
+    params.rel_position_stride, params.rel_head_stride = rel.stride(0), rel.stride(1)
+    params.lengths = lengths.data_ptr()
+    params.batch, params.tokens, params.heads, params.head_dim = batch, tokens, heads, head_dim
+    params.chunk, params.past, params.future, params.rel_positions = chunk, past, future, rel.shape[0]
+    params.softcap, params.invalid = softcap, invalid
+    lib = _lib.load()
+    _lib.check(lib.asrattn_local(ctypes.byref(params), _stream(device)), "asrattn_local")
+    return out
+
+
 def greedy_choice(logits: Tensor, suppress: Tensor | None = None) -> tuple[Tensor, Tensor]:
     """Greedy next token per row of float32 ``logits`` ``(rows, vocab)`` and
     its log-probability, in one pass (``asrattn_choose``): the argmax (first
@@ -589,6 +651,14 @@ def greedy_choice(logits: Tensor, suppress: Tensor | None = None) -> tuple[Tenso
 # (calls on one device run in stream order); grown buffers are kept alive
 # because graphs captured earlier still hold their addresses.
 _workspaces: dict[torch.device, list[Tensor]] = {}
+
+
+def decode_supported(dtype: torch.dtype, head_dim: int, group: int) -> bool:
+    """Whether the decode kernel takes this element type, head size and
+    number of query heads per kv head (``decode_supported`` of the library:
+    head_dim 64/128/256, and 512 in bfloat16; 1, 2, 4 or 8 heads)."""
+    sizes = (64, 128, 256, 512) if dtype == torch.bfloat16 else (64, 128, 256)
+    return dtype in _DTYPES and head_dim in sizes and group in (1, 2, 4, 8)
 
 
 def decode_workspace(nbytes: int, device: torch.device) -> Tensor:

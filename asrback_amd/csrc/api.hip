@@ -139,6 +139,8 @@ int check_fwd(const asrattn_fwd_params* params, bool* empty) {
     return fail(ASRATTN_ERR_INVALID, "causal must be 0, 1 or 2, got %d", p.causal);
   if ((p.cu_seqlens_q == nullptr) != (p.cu_seqlens_k == nullptr))
     return fail(ASRATTN_ERR_INVALID, "cu_seqlens_q and cu_seqlens_k must both be set or both be NULL");
+  if (p.window < 0 || (p.window > 0 && p.causal == ASRATTN_CAUSAL_NONE))
+    return fail(ASRATTN_ERR_INVALID, "window must be >= 0, and > 0 only with causal attention (got %d)", p.window);
   *empty = p.batch == 0 || p.max_len_q == 0;
   if (*empty) return ASRATTN_OK;
   if (p.q == nullptr || p.k == nullptr || p.v == nullptr || p.out == nullptr)
@@ -151,7 +153,8 @@ int check_fwd(const asrattn_fwd_params* params, bool* empty) {
                 "q, k, v and out need 16-byte aligned pointers and strides that are multiples of 16 bytes");
   const bool generic = (p.flags & ASRATTN_FWD_FORCE_VALU) != 0;
   if ((generic || !asrattn::fwd_ring_supported(p)) && !asrattn::fwd_valu_supported(p.dtype, p.head_dim))
-    return fail(ASRATTN_ERR_UNSUPPORTED, "no forward kernel for head_dim %d (supported: 64, 128)", p.head_dim);
+    return fail(ASRATTN_ERR_UNSUPPORTED, "no forward kernel for head_dim %d (supported: 64, 128, 256, 512)",
+                p.head_dim);
   return ASRATTN_OK;
 }
 
@@ -324,6 +327,25 @@ int asrattn_decode_append(const asrattn_decode_params* params, const asrattn_app
                           void* workspace, size_t workspace_bytes, void* stream) {
   if (append == nullptr) return fail(ASRATTN_ERR_INVALID, "append parameters must be non-NULL");
   return run_decode(params, append, nullptr, workspace, workspace_bytes, stream, "asrattn_decode_append");
+}
+
+int asrattn_local(const asrattn_local_params* params, void* stream) {
+  if (params == nullptr) return fail(ASRATTN_ERR_INVALID, "params is NULL");
+  const asrattn_local_params& p = *params;
+  if (p.batch < 0 || p.tokens < 0 || p.heads <= 0 || p.head_dim <= 0)
+    return fail(ASRATTN_ERR_INVALID, "batch, tokens, heads and head_dim must be >= 0 (heads, head_dim > 0)");
+  if (p.chunk <= 0 || p.past < 0 || p.future < 0 || p.rel_positions < 0 || p.rel_positions > p.past + p.future + 2)
+    return fail(ASRATTN_ERR_INVALID,
+                "chunk must be > 0, past and future >= 0, and 0 <= rel_positions <= past + future + 2");
+  if (!(p.softcap > 0.f) || !std::isfinite(p.softcap) || std::isnan(p.invalid))
+    return fail(ASRATTN_ERR_INVALID, "softcap must be positive and finite, invalid not NaN");
+  if (asrattn::local_lds_bytes(p) > 65536)
+    return fail(ASRATTN_ERR_UNSUPPORTED, "a block's keys, values, queries and relative keys exceed 64 KB of LDS");
+  if (p.batch == 0 || p.tokens == 0) return ok();
+  if (p.q == nullptr || p.k == nullptr || p.v == nullptr || p.out == nullptr || p.lengths == nullptr ||
+      (p.rel_positions > 0 && p.rel == nullptr))
+    return fail(ASRATTN_ERR_INVALID, "q, k, v, out, lengths (and rel) must be non-NULL");
+  return from_hip(asrattn::launch_local(p, static_cast<hipStream_t>(stream)), "asrattn_local");
 }
 
 int asrattn_decode_paged(const asrattn_decode_params* params, const asrattn_append_params* append,

@@ -60,4 +60,12 @@ __device__ __forceinline__ int visible_keys(const asrattn_fwd_params& p, const S
   return max(0, min(s.n_k, r + 1 + shift));
 }
 
+// The first key query row r of a sequence sees (window > 0, causal): keys
+// first_key(r) <= j < visible_keys(r).
+__device__ __forceinline__ int first_key(const asrattn_fwd_params& p, const SeqView& s, int r) {
+  if (p.window <= 0 || p.causal == ASRATTN_CAUSAL_NONE) return 0;
+  const int shift = p.causal == ASRATTN_CAUSAL_BOTTOM_RIGHT ? s.n_k - s.len_q : 0;
+  return max(0, r + 1 + shift - p.window);
+}
+
 }  // namespace asrattn

@@ -585,6 +585,7 @@ hipError_t launch_hd(const FwdArgs& a, hipStream_t stream) {
 
 bool fwd_ring_supported(const asrattn_fwd_params& p) {
   if (p.dtype != ASRATTN_BF16 || (p.head_dim != 64 && p.head_dim != 128)) return false;
+  if (p.window > 0) return false;  // sliding windows run on the vector-ALU kernel
   // A key row must end before the next one starts for the resource bound
   // (last visible key's row end) to cover every visible key.
   if (p.k_token_stride < p.head_dim || p.v_token_stride < p.head_dim) return false;

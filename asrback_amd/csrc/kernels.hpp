@@ -41,6 +41,11 @@ hipError_t launch_choose(const float* logits, int64_t rows, int64_t vocab, int64
 hipError_t launch_fwd_valu(const asrattn_fwd_params& p, hipStream_t stream);
 bool fwd_valu_supported(int dtype, int head_dim);
 
+// Blocked local attention with relative position scores (asrattn_local),
+// and the LDS it stages per workgroup.
+hipError_t launch_local(const asrattn_local_params& p, hipStream_t stream);
+size_t local_lds_bytes(const asrattn_local_params& p);
+
 // SAN-M's FSMN memory on its own (fp32 or bf16, head_dim 64 or 128, kernel
 // size at most kFsmnMaxKernel) for the padded layout of p (values p.v, frame
 // counts p.seqused_k).

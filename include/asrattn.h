@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define ASRATTN_ABI_VERSION 5
+#define ASRATTN_ABI_VERSION 7
 
 enum asrattn_status {
   ASRATTN_OK = 0,
@@ -72,6 +72,8 @@ enum asrattn_causal {
  * stride is ignored and the sequence has cu_seqlens_q[b+1] - cu_seqlens_q[b]
  * queries (at most max_len_q).  seqused_k (int32[batch], device, optional)
  * caps the keys sequence b uses.  A query with no visible key gets zeros.
+ * head_dim 64 or 128, and 256 or 512 on the vector-ALU kernel (Gemma 4's
+ * sliding and full layers, gemma4.py:552-559, scale 1.0).
  *
  * Replaces:
  *   F.scaled_dot_product_attention   src/asrback/models/whisper.py:102-104
@@ -106,6 +108,9 @@ typedef struct asrattn_fwd_params {
   int32_t dtype;  /* enum asrattn_dtype */
   float scale;    /* softmax scale; torch's default is 1 / sqrt(head_dim) */
   int32_t flags;  /* 0, or ASRATTN_FWD_FORCE_VALU */
+  int32_t window; /* > 0 (causal only): query i also sees no key more than
+                     window - 1 before its last visible one (sliding-window
+                     attention, gemma4.py:1231-1234); 0: none */
 } asrattn_fwd_params;
 
 int asrattn_fwd(const asrattn_fwd_params* params, void* stream);
@@ -311,6 +316,53 @@ int asrattn_decode_paged(const asrattn_decode_params* params, const asrattn_appe
  */
 int asrattn_choose(const float* logits, int64_t rows, int64_t vocab, int64_t row_stride, const uint8_t* suppress,
                    int64_t* token, float* logprob, void* stream);
+
+/*
+ * Blocked local attention with relative position scores, in float32 (Gemma 4's
+ * audio encoder).  Queries form blocks of `chunk` tokens; block u's context
+ * slots t = 0 .. chunk + past + future - 1 hold keys u * chunk - past + t.
+ * For query i = u * chunk + c of sequence b, head h:
+ *
+ *   s[t]   = q_i . k_key + (0 <= t - c < rel_positions ? q_i . rel[t - c] : 0)
+ *   s[t]   = tanh(s[t] / softcap) * softcap
+ *   s[t]   = invalid  unless  (0 <= i - key < past  or  0 < key - i < future)
+ *                     and 0 <= key < lengths[b]
+ *   out[b, i, h, :] = sum_t softmax(s)[t] v_key        (keys outside 0 ..
+ *                     tokens - 1 are zeros)
+ *
+ * q, k, v, out: (batch, tokens, heads, head_dim) with element strides;
+ * rel: (rel_positions, heads, head_dim), relative keys of distances
+ * past .. 0 (row r: distance past - r; the reference's sinusoids through
+ * relative_k_proj); lengths: int32[batch], device.  The module scales q and
+ * k before the call, as the reference does.  Requires rel_positions <= past
+ * + future + 2 (the reference's relative shift then never wraps into the
+ * previous row) and a block's staged data within 64 KB of LDS.
+ *
+ * Replaces (the attention of AudioAttention.forward):
+ *   context gathering, content and relative scores, the relative shift,
+ *   the soft cap, the mask and the softmax
+ *                                    src/asrback/models/gemma4.py:240-282
+ */
+typedef struct asrattn_local_params {
+  const float* q;
+  const float* k;
+  const float* v;
+  const float* rel;
+  float* out;
+  int64_t q_batch_stride, q_token_stride, q_head_stride;
+  int64_t k_batch_stride, k_token_stride, k_head_stride;
+  int64_t v_batch_stride, v_token_stride, v_head_stride;
+  int64_t o_batch_stride, o_token_stride, o_head_stride;
+  int64_t rel_position_stride, rel_head_stride;
+  const int32_t* lengths;
+  int32_t batch, tokens, heads, head_dim;
+  int32_t chunk, past, future, rel_positions;
+  float softcap;
+  float invalid; /* the score of slots a query may not see (the reference's
+                    attention_invalid_logits_value) */
+} asrattn_local_params;
+
+int asrattn_local(const asrattn_local_params* params, void* stream);
 
 /* Message of the last failed call on this thread ("" if none). */
 const char* asrattn_last_error(void);

@@ -7,8 +7,8 @@ modules build, and the modules and greedy decoding loops around them.  Each
 function cites the reference file:line it follows.
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s CPU-baseline
-leg may import it, and only as the checker (or, in ``bench.py``, as the timed
-CPU baseline).  The product (``asrback_amd``) never imports it and has no CPU
+leg may import it, and only as the reference results are compared with (or,
+in ``bench.py``, as the timed CPU baseline).  The product (``asrback_amd``) never imports it and has no CPU
 fallback.
 
 Pinning (what checks each function against something other than itself):
@@ -29,6 +29,11 @@ Pinning (what checks each function against something other than itself):
   Qwen3 text attention; pinned by padding invariance (a padded batch equals
   per-sequence runs), FSMN against an explicit loop, RMSNorm against its
   formula, and the GQA/RoPE invariants above.
+* ``gemma4`` -- Gemma 4's blocked audio attention (the reference's padding,
+  unfold and Transformer-XL relative shift) pinned against a float64 loop
+  over queries and keys written from the definition; the text attention's
+  masks pinned against explicit loops, a step against the prompt pass's row
+  and against plain attention over the window's keys.
 
 The reference's Python cannot be imported here (its ``asrfront`` dependency
 is absent); it was read, never run.

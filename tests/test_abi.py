@@ -42,6 +42,7 @@ def test_header_declares_expected_entry_points():
         "asrattn_decode",
         "asrattn_decode_append",
         "asrattn_decode_paged",
+        "asrattn_local",
         "asrattn_choose",
         "asrattn_decode_workspace_size",
         "asrattn_decode_num_splits",
@@ -87,14 +88,14 @@ def _c_layout(struct: str, fields: list[str]) -> dict[str, int]:
     return {k: int(v) for k, v in (line.split() for line in out.splitlines())}
 
 
-@pytest.mark.parametrize("name", ["FwdParams", "DecodeParams", "AppendParams", "FsmnParams", "PagedKV"])
+@pytest.mark.parametrize("name", ["FwdParams", "DecodeParams", "AppendParams", "FsmnParams", "PagedKV", "LocalParams"])
 def test_ctypes_structs_match_c_layout(name):
     from asrback_amd import _lib
 
     cls = getattr(_lib, name)
     struct = {"FwdParams": "asrattn_fwd_params", "DecodeParams": "asrattn_decode_params",
               "AppendParams": "asrattn_append_params", "FsmnParams": "asrattn_fsmn_params",
-              "PagedKV": "asrattn_paged_kv"}[name]
+              "PagedKV": "asrattn_paged_kv", "LocalParams": "asrattn_local_params"}[name]
     fields = [f for f, _ in cls._fields_]
     layout = _c_layout(struct, fields)
     assert layout.pop("sizeof") == ctypes.sizeof(cls)
@@ -241,6 +242,37 @@ def test_invalid_paged_arguments_are_reported(lib):
     pk.k_page_stride, pk.page_size, pk.bt_stride = 64 * 256, 16, 64
     assert lib.asrattn_decode_paged(ctypes.byref(p), None, ctypes.byref(pk), None, 0, None) == _lib.ERR_UNSUPPORTED
     assert b">= 32" in lib.asrattn_last_error()
+
+
+def test_invalid_window_and_local_arguments_are_reported(lib):
+    """Window and blocked-local-attention checks, before any device call."""
+    from asrback_amd import _lib
+
+    f = _lib.FwdParams()
+    f.batch, f.heads_q, f.heads_kv, f.head_dim = 1, 8, 1, 256
+    f.max_len_q = f.max_len_k = 4
+    f.dtype, f.scale, f.window = _lib.BF16, 1.0, 512
+    assert lib.asrattn_fwd(ctypes.byref(f), None) == _lib.ERR_INVALID  # a window needs causal attention
+    assert b"window" in lib.asrattn_last_error()
+    f.causal, f.window = _lib.CAUSAL_TOP_LEFT, -1
+    assert lib.asrattn_fwd(ctypes.byref(f), None) == _lib.ERR_INVALID
+    d = _lib.DecodeParams()
+    d.batch, d.heads_q, d.heads_kv, d.head_dim, d.max_len_k = 1, 8, 1, 512, 16
+    d.dtype, d.scale, d.window = _lib.F32, 1.0, 0
+    assert lib.asrattn_decode(ctypes.byref(d), None, 0, None) == _lib.ERR_UNSUPPORTED  # fp32 at 512
+    d.dtype, d.window = _lib.BF16, -3
+    assert lib.asrattn_decode(ctypes.byref(d), None, 0, None) == _lib.ERR_INVALID
+    p = _lib.LocalParams()
+    p.batch, p.tokens, p.heads, p.head_dim = 1, 10, 2, 64
+    p.chunk, p.past, p.future, p.rel_positions, p.softcap, p.invalid = 12, 12, 0, 15, 50.0, -1e9
+    assert lib.asrattn_local(ctypes.byref(p), None) == _lib.ERR_INVALID  # 15 > past + future + 2
+    p.rel_positions, p.softcap = 13, 0.0
+    assert lib.asrattn_local(ctypes.byref(p), None) == _lib.ERR_INVALID
+    p.softcap, p.head_dim = 50.0, 1024  # the block's staging exceeds 64 KB of LDS
+    assert lib.asrattn_local(ctypes.byref(p), None) == _lib.ERR_UNSUPPORTED
+    p.head_dim = 64
+    assert lib.asrattn_local(ctypes.byref(p), None) == _lib.ERR_INVALID  # NULL tensors
+    assert b"non-NULL" in lib.asrattn_last_error()
 
 
 def test_workspace_size_and_split_choice(lib):

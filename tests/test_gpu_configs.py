@@ -544,6 +544,37 @@ def test_gemma_decode_window_and_head_sizes(ops, device, dtype, hd, heads_q, hea
     assert max_rel_err(out, ref) < TOL[dtype]
 
 
+@pytest.mark.parametrize(
+    "dtype,hd,heads_q,heads_kv,window",
+    [
+        (torch.bfloat16, 256, 8, 1, 512),
+        (torch.bfloat16, 512, 8, 1, None),
+        (torch.bfloat16, 512, 8, 2, None),
+        (torch.float32, 256, 8, 2, 512),
+        (torch.float32, 512, 8, 1, 100),
+        (torch.bfloat16, 128, 16, 8, 100),
+    ],
+)
+def test_gemma_prefill_window_and_head_sizes(ops, device, dtype, hd, heads_q, heads_kv, window):
+    """Gemma 4's padded prompt pass (gemma4.py:552-559, masks :1227-1235):
+    causal, keys before each prompt's size, the sliding window, scale 1.0,
+    grouped-query attention, head_dim 256/512, against the oracle's masked
+    SDPA on the prompts' own rows."""
+    say("gemma prefill", dtype, hd, heads_q, heads_kv, window)
+    batch, length = 3, 700
+    sizes = torch.tensor([700, 513, 37])
+    q = randn(batch, length, heads_q, hd, seed=121, dtype=dtype) * 0.1
+    k = randn(batch, length, heads_kv, hd, seed=122, dtype=dtype)
+    v = randn(batch, length, heads_kv, hd, seed=123, dtype=dtype)
+    mask = oa.gemma_prefill_mask(sizes, length, window)
+    ref = oa.sdpa(q.float().transpose(1, 2), k.float().transpose(1, 2), v.float().transpose(1, 2),
+                  attn_mask=mask, scale=1.0, enable_gqa=True).transpose(1, 2)
+    out = ops.flash(q.to(device), k.to(device), v.to(device), causal=1, seqused_k=sizes.int().to(device),
+                    scale=1.0, window=window).cpu()
+    for b, n in enumerate(sizes.tolist()):
+        assert max_rel_err(out[b, :n], ref[b, :n]) < TOL[dtype]
+
+
 def test_gemma_decode_append_window(ops, device):
     """The appending step with a window: the new key is the last of the
     window's keys, and only cache keys position - window + 1 .. position - 1

@@ -261,3 +261,46 @@ def test_fsmn_matches_explicit_loop():
                 ref[b, t, c] = acc
     ref = (ref + masked) * keep
     torch.testing.assert_close(out, ref, rtol=1e-12, atol=1e-12)
+
+
+# --- Gemma 4 blocked audio attention ------------------------------------------
+
+
+@pytest.mark.parametrize("frames,lengths,future", [(29, [29, 17, 1], 0), (25, [25, 9], 3)])
+def test_gemma_local_attention_matches_definition(frames, lengths, future):
+    """The reference's unfold + relative-shift route (gemma4.py:256-282)
+    equals the definition evaluated query by query (relative row t - c,
+    i.e. distance past - r; invalid score outside each query's window and the
+    sequence's length), including padded queries that see no key."""
+    from oracle import gemma4 as og
+
+    chunk, past, heads, head_dim = 4, 5, 2, 8
+    g = torch.Generator().manual_seed(14)
+    q, k, v = (torch.randn(len(lengths), frames, heads, head_dim, generator=g, dtype=torch.float64)
+               for _ in range(3))
+    rel_rows = (chunk + past + future) // 2 + 1
+    relative = torch.randn(rel_rows, heads, head_dim, generator=g, dtype=torch.float64)
+    lengths_t = torch.tensor(lengths)
+    mask = og.blocked_mask(lengths_t, frames, chunk, past, future)
+    out = og.local_attention(q, k, v, relative, mask, chunk, past, future, 7.0, -1e9)
+    ref = og.local_attention_loops(q, k, v, relative, lengths_t, chunk, past, future, 7.0, -1e9)
+    assert max_rel_err(out, ref) < 1e-12
+
+
+def test_gemma_relative_positions_and_window():
+    """Relative row r holds the sinusoids of distance context // 2 - r, and a
+    query's visible keys are itself and the past - 1 before it
+    (gemma4.py:380-396, :223-240)."""
+    from oracle import gemma4 as og
+
+    table = og.relative_positions(8, chunk=12, context_left=13, context_right=0)
+    assert table.shape == (13, 8)
+    assert torch.equal(table[-1], torch.cat((torch.zeros(4), torch.ones(4))))  # distance 0: sin 0, cos 0
+    inverse = torch.exp(torch.arange(4) * -(math.log(10000) / 3))
+    assert torch.allclose(table[0, :4], torch.sin(12 * inverse))
+    mask = og.blocked_mask(torch.tensor([40]), 40, 12, 12, 0)
+    allowed = ~mask[0, 0]
+    for i in range(40):
+        u, c = divmod(i, 12)
+        keys = [u * 12 - 12 + t for t in range(24) if bool(allowed[u, c, t])]
+        assert keys == list(range(max(0, i - 11), i + 1))
