@@ -17,11 +17,14 @@ a (28, 64, 1024, 8, 128) cache, 128 steps; also over a paged cache of
 1500 frames), in algorithmic HBM GB/s (K and V of the keys each row uses,
 plus q and o), and the Qwen3 step with its prologue (per-head RMSNorm and
 rotary embedding of q and k, the cache write) fused into the decode launch,
-timed beside the unfused sequence of ops, and the greedy token choice over
-Qwen3's (64, 151936) logits in one pass.  ``secondary`` adds the SenseVoice
-attention with its FSMN memory fused into the same launch (timed beside the
-reference's ops for both outputs) and Whisper large-v3-turbo's encoder
-attention (20 heads x 64, 1500 frames, batch 16, 32 layers).
+timed beside the unfused sequence of ops, the greedy token choice over
+Qwen3's (64, 151936) logits in one pass, and Gemma 4's decoder step (sliding
+layers over a 512-key window at head_dim 256, full layers at 512).
+``secondary`` adds the SenseVoice attention with its FSMN memory fused into
+the same launch (timed beside the reference's ops for both outputs), Whisper
+large-v3-turbo's encoder attention (20 heads x 64, 1500 frames, batch 16, 32
+layers), Qwen3's causal grouped-query prompt pass and Gemma 4's blocked
+local audio attention.
 
 ``cpu_baseline`` times the CPU restatement of the reference's attention
 (torch SDPA with the key-padding mask, float32, the reference's CPU path) on
@@ -207,6 +210,157 @@ class WhisperTurboEncoder(Workload):
     def config(self) -> dict:
         return {"workload": self.name, "batch": self.batch, "heads": self.heads, "head_dim": self.head_dim,
                 "layers": self.layers, "frames": self.length}
+
+
+class Qwen3Prefill(Workload):
+    """Qwen3-ASR-1.7B prompt pass (qwen3_asr.py:374-390 via ``attend``,
+    :152-166): 8 packed prompts of 390 + U{10..40} tokens, q ``(tokens, 16,
+    128)`` over k/v ``(tokens, 8, 128)``, causal (``window_size=(-1, 0)``)
+    and grouped-query, 28 layers.  Value: causal TFLOP/s, ``4 * 128 * 16 *
+    P (P + 1) / 2`` per prompt and layer (each query over the keys it sees)."""
+
+    name = "qwen3-asr-1.7b-prefill-attention"
+    unit = "TFLOP/s"
+    bound = "mfma"
+    kernel = "fwd_ring_kernel"
+
+    def __init__(self, torch, attention, seed: int = 4) -> None:
+        rng = np.random.default_rng(seed)
+        self.prompts = (390 + rng.integers(10, 41, size=8)).astype(np.int64)
+        self.heads_q, self.heads_kv, self.head_dim, self.layers = 16, 8, 128, 28
+        tokens = int(self.prompts.sum())
+        starts = np.concatenate(([0], np.cumsum(self.prompts))).astype(np.int32)
+        self.cu = torch.from_numpy(starts).cuda()
+        self.longest = int(self.prompts.max())
+        g = torch.Generator(device="cuda").manual_seed(seed)
+        self.q = [torch.randn((tokens, self.heads_q, self.head_dim), generator=g, device="cuda", dtype=torch.bfloat16)
+                  for _ in range(self.layers)]
+        self.kv = [torch.randn((2, tokens, self.heads_kv, self.head_dim), generator=g, device="cuda",
+                               dtype=torch.bfloat16) for _ in range(self.layers)]
+        self.attention = attention
+        self.launches = self.layers
+        per_layer = float(sum(4 * self.head_dim * self.heads_q * int(p) * (int(p) + 1) // 2 for p in self.prompts))
+        self.work_per_step = per_layer * self.layers
+
+    def run(self) -> None:
+        for layer in range(self.layers):
+            k, v = self.kv[layer]
+            self.attention.varlen_attn(self.q[layer], k, v, self.cu, self.cu, self.longest, self.longest,
+                                       window_size=(-1, 0), enable_gqa=True)
+
+    def config(self) -> dict:
+        return {"workload": self.name, "prompts": 8, "prompt_tokens": "390 + U{10..40}", "heads_q": self.heads_q,
+                "heads_kv": self.heads_kv, "head_dim": self.head_dim, "layers": self.layers, "causal": "bottom-right"}
+
+
+class Gemma4AudioAttention(Workload):
+    """Gemma 4's blocked local audio attention (gemma4.py:240-282) with
+    transformers' ``Gemma4AudioConfig`` defaults: 8 heads x 128, 12 layers,
+    blocks of 12 tokens seeing the 12 before them, 13 relative keys, soft cap
+    50, float32 as the reference computes it; 8 windows of 30 s (750 tokens,
+    one a shorter tail).  Value: algorithmic HBM GB/s (q, k, v read and the
+    output written once, plus the relative keys)."""
+
+    name = "gemma4-audio-local-attention"
+    unit = "GB/s"
+    bound = "hbm"
+    kernel = "local_kernel"
+
+    def __init__(self, torch, attention, seed: int = 5) -> None:
+        self.batch, self.tokens, self.heads, self.head_dim, self.layers = 8, 750, 8, 128, 12
+        self.chunk, self.past, self.rel_positions = 12, 12, 13
+        lengths = np.full(self.batch, self.tokens, dtype=np.int32)
+        lengths[-1] = 412
+        self.lengths = torch.from_numpy(lengths).cuda()
+        shape = (self.batch, self.tokens, self.heads, self.head_dim)
+        g = torch.Generator(device="cuda").manual_seed(seed)
+        self.qkv = [[torch.randn(shape, generator=g, device="cuda") for _ in range(3)] for _ in range(self.layers)]
+        self.rel = [torch.randn((self.rel_positions, self.heads, self.head_dim), generator=g, device="cuda")
+                    for _ in range(self.layers)]
+        self.out = torch.empty(shape, device="cuda")
+        self.attention = attention
+        self.launches = self.layers
+        elements = self.batch * self.tokens * self.heads * self.head_dim
+        per_layer = 4.0 * (4 * elements + self.rel_positions * self.heads * self.head_dim)
+        self.work_per_step = per_layer * self.layers
+
+    def run(self) -> None:
+        for layer in range(self.layers):
+            q, k, v = self.qkv[layer]
+            self.attention.local_attention(q, k, v, self.rel[layer], self.lengths, chunk=self.chunk, past=self.past,
+                                           future=0, softcap=50.0, invalid=-1e9, out=self.out)
+
+    def config(self) -> dict:
+        return {"workload": self.name, "batch": self.batch, "tokens": self.tokens, "heads": self.heads,
+                "head_dim": self.head_dim, "layers": self.layers, "chunk": self.chunk, "past": self.past,
+                "dtype": "float32"}
+
+
+class Gemma4TextDecode(Workload):
+    """Gemma 4's decoder step (gemma4.py:534-587, ``scale=1.0``) with
+    transformers' ``Gemma4TextConfig`` defaults: 30 layers, five sliding to
+    one full, 8 query heads over 4 kv heads; sliding layers head_dim 256 over
+    the last 512 keys, full layers head_dim 512 over every key.  32 rows
+    (the reference's default batch in bfloat16, gemma4.py:874-875) of a
+    ``(32, 1280, 4, head_dim)`` cache per layer, prompts of 800 + U{0..40}
+    tokens (a 30 s window's prompt), 128 steps.  Value: algorithmic HBM GB/s
+    (K and V of the keys each row's window holds, plus q and o)."""
+
+    name = "gemma4-text-decode-attention"
+    unit = "GB/s"
+    bound = "hbm"
+    kernel = "decode_kernel"
+
+    def __init__(self, torch, attention, seed: int = 6, steps: int = 128) -> None:
+        rng = np.random.default_rng(seed)
+        self.torch = torch
+        self.batch, self.heads_q, self.heads_kv, self.layers = 32, 8, 4, 30
+        self.cache_length, self.steps, self.window = 1280, steps, 512
+        self.full = [(i + 1) % 6 == 0 for i in range(self.layers)]
+        self.prompts = (800 + rng.integers(0, 41, size=self.batch)).astype(np.int64)
+        g = torch.Generator(device="cuda").manual_seed(seed)
+        self.cache, self.q = [], []
+        for full in self.full:
+            hd = 512 if full else 256
+            shape = (2, self.batch, self.cache_length, self.heads_kv, hd)
+            self.cache.append(torch.randn(shape, generator=g, device="cuda", dtype=torch.bfloat16))
+            self.q.append(torch.randn((self.batch, self.heads_q, hd), generator=g, device="cuda", dtype=torch.bfloat16))
+        self.out = {hd: torch.empty((self.batch, self.heads_q, hd), device="cuda", dtype=torch.bfloat16)
+                    for hd in (256, 512)}
+        self.start = torch.from_numpy(self.prompts - 1).cuda()
+        self.positions = self.start.clone()
+        self.used = torch.empty(self.batch, dtype=torch.int32, device="cuda")
+        self.attention = attention
+        self.launches = self.layers
+        self.step_bytes = []
+        for t in range(self.steps):
+            total = 0.0
+            for full in self.full:
+                hd = 512 if full else 256
+                for p in self.prompts:
+                    keys = int(p) + t + 1
+                    keys = keys if full else min(keys, self.window)
+                    total += 2 * self.heads_kv * hd * 2 * keys + 2 * self.heads_q * hd * 2
+            self.step_bytes.append(total)
+        self.work_per_step = float(np.mean(self.step_bytes))
+
+    def reset(self) -> None:
+        self.positions.copy_(self.start)
+
+    def run(self) -> None:
+        self.positions.add_(1)
+        self.used.copy_(self.positions + 1)
+        for layer, full in enumerate(self.full):
+            k, v = self.cache[layer]
+            hd = k.shape[-1]
+            self.attention.decode(self.q[layer], k, v, seqused_k=self.used, scale=1.0,
+                                  window=None if full else self.window, out=self.out[hd])
+
+    def config(self) -> dict:
+        return {"workload": self.name, "batch": self.batch, "heads_q": self.heads_q, "heads_kv": self.heads_kv,
+                "head_dim": "256 (sliding, window 512) / 512 (full)", "layers": self.layers,
+                "full_layers": sum(self.full), "cache_length": self.cache_length, "prompt_tokens": "800 + U{0..40}",
+                "steps": self.steps}
 
 
 class Qwen3Decode(Workload):
@@ -554,8 +708,8 @@ def roofline(workload: Workload, ms_per_step: float, work_per_step: float) -> di
 
 
 def measure(torch, workload: Workload, steps: int, warmup: int) -> dict:
-    if isinstance(workload, Qwen3Decode):
-        # The 128-step decode: the timed steps advance the positions.
+    if hasattr(workload, "step_bytes"):
+        # The 128-step decodes: the timed steps advance the positions.
         steps = min(steps, workload.steps)
         ms = time_graph(torch, workload, steps, min(warmup, workload.steps), reset=workload.reset)
         work = float(np.mean(workload.step_bytes[:steps]))
@@ -699,7 +853,8 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--only", choices=["sensevoice", "sensevoice-fsmn", "turbo", "qwen3", "qwen3-paged",
-                                           "qwen3-fused", "whisper-small", "choice", "copy"],
+                                           "qwen3-fused", "qwen3-prefill", "whisper-small", "choice",
+                                           "gemma4-audio", "gemma4-decode", "copy"],
                         default=None,
                         help="measure one workload only (for profiling)")
     parser.add_argument("--sweep", action="store_true",
@@ -732,6 +887,9 @@ def main() -> int:
         "qwen3": Qwen3Decode,
         "qwen3-paged": Qwen3DecodePaged,
         "qwen3-fused": Qwen3DecodeStepFused,
+        "qwen3-prefill": Qwen3Prefill,
+        "gemma4-audio": Gemma4AudioAttention,
+        "gemma4-decode": Gemma4TextDecode,
         "choice": GreedyChoice,
         "whisper-small": WhisperSmallDecoderStep,
         "copy": CopyCalibration,
@@ -747,12 +905,13 @@ def main() -> int:
     head = measure(torch, SenseVoiceEncoder(torch, attention), args.steps, args.warmup)
     torch.cuda.empty_cache()
     decode = []
-    for cls in (Qwen3Decode, Qwen3DecodePaged, Qwen3DecodeStepFused, WhisperSmallDecoderStep, GreedyChoice):
+    for cls in (Qwen3Decode, Qwen3DecodePaged, Qwen3DecodeStepFused, WhisperSmallDecoderStep, GreedyChoice,
+                Gemma4TextDecode):
         log(f"bench: {cls.name}")
         decode.append(measure(torch, cls(torch, attention), args.steps, args.warmup))
         torch.cuda.empty_cache()
     secondary = []
-    for cls in (SenseVoiceAttentionFsmn, WhisperTurboEncoder):
+    for cls in (SenseVoiceAttentionFsmn, WhisperTurboEncoder, Qwen3Prefill, Gemma4AudioAttention):
         log(f"bench: {cls.name}")
         secondary.append(measure(torch, cls(torch, attention), args.steps, args.warmup))
         torch.cuda.empty_cache()

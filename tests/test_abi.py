@@ -286,6 +286,10 @@ def test_workspace_size_and_split_choice(lib):
     p.dtype, p.scale = _lib.BF16, 0.125
     assert lib.asrattn_decode_num_splits(ctypes.byref(p)) == 1
     assert lib.asrattn_decode_workspace_size(ctypes.byref(p)) == 0
+    # Gemma 4's 32 rows x 4 kv heads (128 pairs) take two splits.
+    p.batch, p.heads_q, p.heads_kv, p.head_dim, p.max_len_k = 32, 8, 4, 256, 1280
+    assert lib.asrattn_decode_num_splits(ctypes.byref(p)) == 2
+    p.head_dim, p.max_len_k = 64, 1500
     p.batch, p.heads_q, p.heads_kv = 1, 6, 6
     splits = lib.asrattn_decode_num_splits(ctypes.byref(p))
     assert splits == 6  # 1500 keys, at least 256 per split
