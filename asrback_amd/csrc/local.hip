@@ -4,13 +4,17 @@
 // runs on the vector ALUs; a layer is bound by reading q, k, v and writing
 // the output once.
 //
-// local_rows_kernel (head_dim 64..256, contexts up to 32 slots): a
-// workgroup takes a run of consecutive blocks of one (sequence, head).  The
-// run's context keys and values (each key serves two blocks) and the head's
-// relative keys are staged in LDS; each query row belongs to four lanes,
-// which hold a quarter of its dimensions in registers, sum their partial
-// dot products with DPP and read key/value rows from LDS at the same
-// addresses as the row's other queries (broadcast reads).
+// local_mfma_kernel (head_dim 64, 128 or 192, blocks of at most 16
+// queries over at most 32 context slots): a workgroup takes a run of
+// consecutive blocks of one (sequence, head), one wave per block.  The run's
+// values (each serves two blocks) and the head's relative keys are staged
+// in LDS, the queries and keys go straight to registers; each wave computes
+// its block's scores, relative terms and weighted values as fp32 matrix
+// products on the matrix cores
+// (v_mfma_f32_16x16x4_f32, fp32 operands and accumulation), transposed as
+// in the bf16 encoder kernel so that a query's scores stay in its lanes:
+//   S^T = K . Q^T and R^T = Rel . Q^T (16 context slots or relative rows x
+//   16 queries per product), P^T from S^T in registers, O^T = V^T . P^T.
 //
 // local_kernel (any other shape): one wave per (block, head, sequence),
 // one (query, slot) score per lane.
@@ -20,152 +24,215 @@
 namespace asrattn {
 namespace {
 
-constexpr int kRowsThreads = 256;
-constexpr int kRowsMaxContext = 32;
-constexpr size_t kRowsLdsBudget = 64 * 1024;
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
-// Sum over the four lanes of a query row (lanes 4k .. 4k + 3).
-__device__ __forceinline__ float quad_sum(float x) {
-  x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0xb1, 0xf, 0xf, false));  // quad_perm 1,0,3,2
-  x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x4e, 0xf, 0xf, false));  // quad_perm 2,3,0,1
-  return x;
+constexpr int kMfmaMaxWaves = 4;
+constexpr int kMfmaMaxContext = 32;  // two 16-slot tiles
+constexpr size_t kMfmaLdsBudget = 64 * 1024;
+
+// 16 x 16 x 4 fp32 product, lane l: A[l % 16][l / 16], B[l / 16][l % 16],
+// D[4 (l / 16) + r][l % 16] (layout checked on the GPU).
+__device__ __forceinline__ f32x4_t mfma16(float a, float b, const f32x4_t& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
-// Dot product of this lane's DPL dimensions of q with an LDS row segment.
-template <int DPL>
-__device__ __forceinline__ float dot_lds(const float* q, const float* row) {
-  float acc = 0.f;
-#pragma unroll
-  for (int d = 0; d < DPL; d += 4) {
-    const float4 r = *reinterpret_cast<const float4*>(row + d);
-    acc = fmaf(q[d], r.x, acc);
-    acc = fmaf(q[d + 1], r.y, acc);
-    acc = fmaf(q[d + 2], r.z, acc);
-    acc = fmaf(q[d + 3], r.w, acc);
-  }
-  return acc;
+// LDS floats of a workgroup of nblk blocks: the values of its rows and 16
+// relative rows (padded with zeros), each row padded by 4 floats so that the
+// value reads of a product (four rows four apart, 16 columns) hit distinct
+// banks; then per wave 16 x 17 relative scores.
+size_t mfma_lds_floats(const asrattn_local_params& p, int nblk) {
+  const size_t rows = (size_t)nblk * p.chunk + p.past + p.future;
+  return (rows + 16) * (p.head_dim + 4) + (size_t)nblk * 16 * 17;
 }
 
-template <int DPL>
-__global__ __launch_bounds__(kRowsThreads) void local_rows_kernel(const asrattn_local_params p, int nblk) {
+// Staging copies in flight per thread (16-byte loads issued before their
+// LDS stores).
+constexpr int kStageBatch = 8;
+
+template <int KS>  // head_dim / 4: k-steps of a product over the head dimensions
+__global__ __launch_bounds__(64 * kMfmaMaxWaves) void local_mfma_kernel(const asrattn_local_params p, int nblk) {
   extern __shared__ float smem[];
-  constexpr int D = 4 * DPL;
+  constexpr int D = 4 * KS, RS = D + 4;
   const int C = p.chunk, ctx = p.chunk + p.past + p.future, R = p.rel_positions;
   const int h = blockIdx.y;
   const int b = blockIdx.z;
-  const int u0 = blockIdx.x * nblk;          // the run's first block
-  const int key0 = u0 * C - p.past;          // key of staged row 0
+  const int u0 = blockIdx.x * nblk;  // the run's first block
+  const int key0 = u0 * C - p.past;  // key of staged row 0
   const int rows = nblk * C + p.past + p.future;
   const int n = min(max(p.lengths[b], 0), p.tokens);  // valid keys of the sequence
   const int tid = threadIdx.x;
-  float* Ks = smem;          // [rows][D]
-  float* Vs = Ks + rows * D;  // [rows][D]
-  float* Rs = Vs + rows * D;  // [R][D]
+  float* Vs = smem;            // [rows][RS]
+  float* Rs = Vs + rows * RS;  // [16][RS]
+  float* Xs = Rs + 16 * RS;    // [wave][16][17]
 
-  // Staged row r holds key key0 + r: zeros outside the sequence's tokens
-  // (the reference's padding).
-  for (int i = tid; i < rows * (D / 4); i += blockDim.x) {
-    const int r = i / (D / 4), d = (i % (D / 4)) * 4;
-    const int key = key0 + r;
-    float4 kk = make_float4(0.f, 0.f, 0.f, 0.f), vv = kk;
-    if (key >= 0 && key < p.tokens) {
-      kk = *reinterpret_cast<const float4*>(p.k + (int64_t)b * p.k_batch_stride + (int64_t)key * p.k_token_stride +
-                                            (int64_t)h * p.k_head_stride + d);
-      vv = *reinterpret_cast<const float4*>(p.v + (int64_t)b * p.v_batch_stride + (int64_t)key * p.v_token_stride +
-                                            (int64_t)h * p.v_head_stride + d);
-    }
-    *reinterpret_cast<float4*>(Ks + r * D + d) = kk;
-    *reinterpret_cast<float4*>(Vs + r * D + d) = vv;
-  }
-  for (int i = tid; i < R * (D / 4); i += blockDim.x) {
-    const int r = i / (D / 4), d = (i % (D / 4)) * 4;
-    *reinterpret_cast<float4*>(Rs + r * D + d) =
-        *reinterpret_cast<const float4*>(p.rel + (int64_t)r * p.rel_position_stride + (int64_t)h * p.rel_head_stride + d);
-  }
+  // Lane (col, m): query column col of the wave's block, head dimensions
+  // [m KS, m KS + KS) -- the k slot m of every product step.
+  const int lane = tid & 63, wave = tid >> 6;
+  const int col = lane & 15, m = lane >> 4;
+  const int u = u0 + wave;
+  const int query = u * C + col;
+  const bool qok = col < C && query < p.tokens;
+  // Every row goes through a buffer resource that ends at the sequence's
+  // last token, so tokens outside [0, tokens) read as zeros (the reference's
+  // padding; offsets of negative keys wrap past the end) with no branch.
+  const uint32_t qts = (uint32_t)p.q_token_stride * 4, kts = (uint32_t)p.k_token_stride * 4;
+  const uint32_t vts = (uint32_t)p.v_token_stride * 4, rps = (uint32_t)p.rel_position_stride * 4;
+  const __amdgpu_buffer_rsrc_t qrs =
+      buffer_rsrc(p.q + (int64_t)b * p.q_batch_stride + (int64_t)h * p.q_head_stride, (uint32_t)p.tokens * qts);
+  const __amdgpu_buffer_rsrc_t krs =
+      buffer_rsrc(p.k + (int64_t)b * p.k_batch_stride + (int64_t)h * p.k_head_stride, (uint32_t)p.tokens * kts);
+  const __amdgpu_buffer_rsrc_t vrs =
+      buffer_rsrc(p.v + (int64_t)b * p.v_batch_stride + (int64_t)h * p.v_head_stride, (uint32_t)p.tokens * vts);
+  const __amdgpu_buffer_rsrc_t rrs = buffer_rsrc(p.rel + (int64_t)h * p.rel_head_stride, (uint32_t)R * rps);
 
-  // This lane: dimensions [quarter DPL, +DPL) of query c of block u0 + ub.
-  const int lq = tid >> 2, quarter = tid & 3;
-  const int ub = lq / C, c = lq % C;
-  const int query = (u0 + ub) * C + c;
-  const bool active = ub < nblk && query < p.tokens;
-  float q[DPL];
+  // The block's query col and the keys of context slots col and 16 + col,
+  // straight into the product operands.  Query columns past the block and
+  // slots past the context read nothing (an offset past every range; their
+  // results are never stored or are dropped from the softmax below).
+  float qv[KS], kv[2][KS];
   {
-    const float* qp = p.q + (int64_t)b * p.q_batch_stride + (int64_t)(active ? query : 0) * p.q_token_stride +
-                      (int64_t)h * p.q_head_stride + quarter * DPL;
+    constexpr uint32_t kNowhere = 0x80000000u;  // past any range (ranges stay below 2^31)
+    const uint32_t dim0 = (uint32_t)m * KS * 4;
+    const uint32_t qo = col < C ? (uint32_t)query * qts + dim0 : kNowhere;
+    const int key = u * C - p.past + col;
+    const uint32_t ko0 = col < ctx ? (uint32_t)key * kts + dim0 : kNowhere;
+    const uint32_t ko1 = 16 + col < ctx ? (uint32_t)(key + 16) * kts + dim0 : kNowhere;
 #pragma unroll
-    for (int d = 0; d < DPL; d += 4) {
-      const float4 t = active ? *reinterpret_cast<const float4*>(qp + d) : make_float4(0.f, 0.f, 0.f, 0.f);
-      q[d] = t.x;
-      q[d + 1] = t.y;
-      q[d + 2] = t.z;
-      q[d + 3] = t.w;
+    for (int d = 0; d < KS; d += 4) {
+      const float4 t = __builtin_bit_cast(float4, buffer_load16(qrs, qo + d * 4));
+      const float4 k0 = __builtin_bit_cast(float4, buffer_load16(krs, ko0 + d * 4));
+      const float4 k1 = __builtin_bit_cast(float4, buffer_load16(krs, ko1 + d * 4));
+      qv[d] = t.x, qv[d + 1] = t.y, qv[d + 2] = t.z, qv[d + 3] = t.w;
+      kv[0][d] = k0.x, kv[0][d + 1] = k0.y, kv[0][d + 2] = k0.z, kv[0][d + 3] = k0.w;
+      kv[1][d] = k1.x, kv[1][d + 1] = k1.y, kv[1][d + 2] = k1.z, kv[1][d + 3] = k1.w;
     }
   }
-  __syncthreads();
-  if (!active) return;  // no barrier follows; DPP partners share the row
 
-  // Scores of the context slots: content q . k plus the relative term
-  // q . rel[t - c] (the reference's relative shift: zero unless 0 <= t - c
-  // < R), soft-capped; slots the query may not see take the invalid value.
-  const float* krow = Ks + ub * C * D + quarter * DPL;  // slot t: staged row ub C + t
-  float s[kRowsMaxContext];
+  // Staged value row r holds key key0 + r, then 16 relative rows (zeros
+  // past R).  Loads go out in batches ahead of their stores; the last
+  // batch's surplus threads repeat the last chunk (same value, same place).
+  const int vchunks = rows * KS;
+  for (int base = tid; base < vchunks; base += kStageBatch * (int)blockDim.x) {
+    float4 x[kStageBatch];
+#pragma unroll
+    for (int j = 0; j < kStageBatch; ++j) {
+      const int i = min(base + j * (int)blockDim.x, vchunks - 1);
+      x[j] = __builtin_bit_cast(float4, buffer_load16(vrs, (uint32_t)(key0 + i / KS) * vts + (uint32_t)(i % KS) * 16));
+    }
+#pragma unroll
+    for (int j = 0; j < kStageBatch; ++j) {
+      const int i = min(base + j * (int)blockDim.x, vchunks - 1);
+      *reinterpret_cast<float4*>(Vs + (i / KS) * RS + (i % KS) * 4) = x[j];
+    }
+  }
+  for (int i = tid; i < 16 * KS; i += blockDim.x)
+    *reinterpret_cast<float4*>(Rs + (i / KS) * RS + (i % KS) * 4) =
+        __builtin_bit_cast(float4, buffer_load16(rrs, (uint32_t)(i / KS) * rps + (uint32_t)(i % KS) * 16));
+  __syncthreads();
+
+  // S^T: context slot 16 nt + col against query column col.
+  f32x4_t st[2];
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    st[nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int d = 0; d < KS; ++d) st[nt] = mfma16(kv[nt][d], qv[d], st[nt]);
+  }
+  // Relative scores R^T[row][query]; lane holds rows 4 m + r of column col.
+  f32x4_t rt = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  {
+    const float* rr = Rs + col * RS + m * KS;
+#pragma unroll
+    for (int d = 0; d < KS; d += 4) {
+      const float4 rv = *reinterpret_cast<const float4*>(rr + d);
+      rt = mfma16(rv.x, qv[d], rt);
+      rt = mfma16(rv.y, qv[d + 1], rt);
+      rt = mfma16(rv.z, qv[d + 2], rt);
+      rt = mfma16(rv.w, qv[d + 3], rt);
+    }
+  }
+  // The reference's relative shift: slot t of query c adds relative row
+  // t - c when 0 <= t - c < R; rows move between lanes through LDS.
+  float* xs = Xs + wave * 16 * 17;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) xs[col * 17 + 4 * m + r] = rt[r];
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+  // Soft cap and mask; slots past the context are not part of the softmax.
+  const float inv_cap = 1.f / p.softcap;
+  float s[8];
   float mx = -__builtin_inff();
 #pragma unroll
-  for (int t = 0; t < kRowsMaxContext; ++t) {
-    if (t < ctx) {
-      float sc = quad_sum(dot_lds<DPL>(q, krow + t * D));
-      const int r = t - c;
-      if (R > 0) {
-        const float pos = quad_sum(dot_lds<DPL>(q, Rs + min(max(r, 0), R - 1) * D + quarter * DPL));
-        sc += (r >= 0 && r < R) ? pos : 0.f;
-      }
-      const float capped = tanhf(sc / p.softcap) * p.softcap;
-      const int key = (u0 + ub) * C - p.past + t;
+  for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int t = 16 * nt + 4 * m + r;
+      const int dr = t - col;
+      const float rel = xs[col * 17 + min(max(dr, 0), 15)];
+      const float sc = st[nt][r] + ((dr >= 0 && dr < R) ? rel : 0.f);
+      const float capped = tanhf(sc * inv_cap) * p.softcap;
+      const int key = u * C - p.past + t;
       const int distance = query - key;
       bool allowed = distance >= 0 && distance < p.past;
       if (p.future > 0) allowed = allowed || (distance < 0 && -distance < p.future);
       allowed = allowed && key >= 0 && key < n;
-      s[t] = allowed ? capped : p.invalid;
-      mx = fmaxf(mx, s[t]);
+      const float v = t >= ctx ? -__builtin_inff() : allowed ? capped : p.invalid;
+      s[4 * nt + r] = v;
+      mx = fmaxf(mx, v);
     }
-  }
-  // Softmax (natural exponent, as F.softmax) and the values' weighted sum.
+  // A query's slots live in lanes col, col + 16, col + 32, col + 48.
+  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
   float sum = 0.f;
 #pragma unroll
-  for (int t = 0; t < kRowsMaxContext; ++t)
-    if (t < ctx) {
-      s[t] = expf(s[t] - mx);
-      sum += s[t];
-    }
-  const float inv = 1.f / sum;
-  float o[DPL];
+  for (int i = 0; i < 8; ++i) {
+    s[i] = expf(s[i] - mx);  // natural exponent, as F.softmax; 0 past the context
+    sum += s[i];
+  }
+  sum += __shfl_xor(sum, 16, 64);
+  sum += __shfl_xor(sum, 32, 64);
+
+  // O^T = V^T . P^T: step (nt, r) takes slot 16 nt + 4 m + r in k slot m,
+  // the same slot this lane's P^T register holds.
+  f32x4_t ot[KS / 4];
 #pragma unroll
-  for (int d = 0; d < DPL; ++d) o[d] = 0.f;
-  const float* vrow = Vs + ub * C * D + quarter * DPL;
+  for (int d = 0; d < KS / 4; ++d) ot[d] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int t = 0; t < kRowsMaxContext; ++t)
-    if (t < ctx) {
-      const float w = s[t] * inv;
+  for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
-      for (int d = 0; d < DPL; d += 4) {
-        const float4 v = *reinterpret_cast<const float4*>(vrow + t * D + d);
-        o[d] = fmaf(w, v.x, o[d]);
-        o[d + 1] = fmaf(w, v.y, o[d + 1]);
-        o[d + 2] = fmaf(w, v.z, o[d + 2]);
-        o[d + 3] = fmaf(w, v.w, o[d + 3]);
+    for (int r = 0; r < 4; ++r) {
+      const int t = 16 * nt + 4 * m + r;
+      const bool in = t < ctx;
+      const float* vr = Vs + min(wave * C + t, rows - 1) * RS + col;
+#pragma unroll
+      for (int d = 0; d < KS / 4; ++d) {
+        const float x = vr[16 * d];
+        ot[d] = mfma16(in ? x : 0.f, s[4 * nt + r], ot[d]);
       }
     }
+  if (!qok) return;
+  const float inv = 1.f / sum;
   float* op = p.out + (int64_t)b * p.o_batch_stride + (int64_t)query * p.o_token_stride +
-              (int64_t)h * p.o_head_stride + quarter * DPL;
+              (int64_t)h * p.o_head_stride + 4 * m;
 #pragma unroll
-  for (int d = 0; d < DPL; d += 4) *reinterpret_cast<float4*>(op + d) = make_float4(o[d], o[d + 1], o[d + 2], o[d + 3]);
+  for (int d = 0; d < KS / 4; ++d)
+    *reinterpret_cast<float4*>(op + 16 * d) =
+        make_float4(ot[d][0] * inv, ot[d][1] * inv, ot[d][2] * inv, ot[d][3] * inv);
 }
 
-// Blocks per workgroup of local_rows_kernel (0: the shape does not fit it).
-int rows_blocks(const asrattn_local_params& p) {
-  const int D = p.head_dim;
-  if (D != 64 && D != 128 && D != 192 && D != 256) return 0;
-  if (p.chunk + p.past + p.future > kRowsMaxContext || 4 * p.chunk > kRowsThreads) return 0;
+// Blocks (waves) per workgroup of local_mfma_kernel; 0: the shape does not
+// fit it.
+int mfma_blocks(const asrattn_local_params& p) {
+  if (p.head_dim != 64 && p.head_dim != 128 && p.head_dim != 192) return 0;
+  if (p.chunk > 16 || p.chunk + p.past + p.future > kMfmaMaxContext || p.rel_positions > 16) return 0;
+  // Buffer offsets are 32-bit, with everything at or past 2^31 out of range
+  // (negative keys, at least -past, wrap to 2^32 - past * stride).
+  const int64_t token_strides[] = {p.q_token_stride, p.k_token_stride, p.v_token_stride};
+  for (int64_t st : token_strides)
+    if (st < p.head_dim || ((int64_t)p.tokens + p.past + 32) * st * 4 >= (1LL << 31)) return 0;
+  if ((int64_t)p.rel_positions * p.rel_position_stride * 4 >= (1LL << 31)) return 0;
   // 16-byte loads and stores of every row.
   const void* ptrs[] = {p.q, p.k, p.v, p.rel, p.out};
   for (const void* ptr : ptrs)
@@ -176,10 +243,8 @@ int rows_blocks(const asrattn_local_params& p) {
                              p.rel_position_stride, p.rel_head_stride};
   for (int64_t st : strides)
     if (st % 4 != 0) return 0;
-  for (int nblk = kRowsThreads / (4 * p.chunk); nblk > 0; --nblk) {
-    const size_t rows = (size_t)nblk * p.chunk + p.past + p.future;
-    if (sizeof(float) * (2 * rows + p.rel_positions) * D <= kRowsLdsBudget) return nblk;
-  }
+  for (int nblk = kMfmaMaxWaves; nblk > 0; --nblk)
+    if (sizeof(float) * mfma_lds_floats(p, nblk) <= kMfmaLdsBudget) return nblk;
   return 0;
 }
 
@@ -284,17 +349,14 @@ size_t local_lds_bytes(const asrattn_local_params& p) {
 
 hipError_t launch_local(const asrattn_local_params& p, hipStream_t stream) {
   const int blocks = (p.tokens + p.chunk - 1) / p.chunk;
-  const int nblk = rows_blocks(p);
+  const int nblk = mfma_blocks(p);
   if (nblk > 0) {
     const dim3 grid((unsigned)((blocks + nblk - 1) / nblk), (unsigned)p.heads, (unsigned)p.batch);
-    const int threads = (4 * nblk * p.chunk + 63) / 64 * 64;
-    const size_t rows = (size_t)nblk * p.chunk + p.past + p.future;
-    const size_t lds = sizeof(float) * (2 * rows + p.rel_positions) * p.head_dim;
+    const size_t lds = sizeof(float) * mfma_lds_floats(p, nblk);
     switch (p.head_dim) {
-      case 64: hipLaunchKernelGGL(local_rows_kernel<16>, grid, dim3(threads), lds, stream, p, nblk); break;
-      case 128: hipLaunchKernelGGL(local_rows_kernel<32>, grid, dim3(threads), lds, stream, p, nblk); break;
-      case 192: hipLaunchKernelGGL(local_rows_kernel<48>, grid, dim3(threads), lds, stream, p, nblk); break;
-      default: hipLaunchKernelGGL(local_rows_kernel<64>, grid, dim3(threads), lds, stream, p, nblk); break;
+      case 64: hipLaunchKernelGGL(local_mfma_kernel<16>, grid, dim3(64 * nblk), lds, stream, p, nblk); break;
+      case 128: hipLaunchKernelGGL(local_mfma_kernel<32>, grid, dim3(64 * nblk), lds, stream, p, nblk); break;
+      default: hipLaunchKernelGGL(local_mfma_kernel<48>, grid, dim3(64 * nblk), lds, stream, p, nblk); break;
     }
     return hipGetLastError();
   }

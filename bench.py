@@ -259,12 +259,15 @@ class Gemma4AudioAttention(Workload):
     blocks of 12 tokens seeing the 12 before them, 13 relative keys, soft cap
     50, float32 as the reference computes it; 8 windows of 30 s (750 tokens,
     one a shorter tail).  Value: algorithmic HBM GB/s (q, k, v read and the
-    output written once, plus the relative keys)."""
+    output written once, plus the relative keys).  ``unfused_ms_per_step``
+    times the reference's ops for the same output (pad, unfold into block
+    contexts, content and relative products, the relative shift, soft cap,
+    mask, softmax, product with the values)."""
 
     name = "gemma4-audio-local-attention"
     unit = "GB/s"
     bound = "hbm"
-    kernel = "local_kernel"
+    kernel = "local_mfma_kernel"
 
     def __init__(self, torch, attention, seed: int = 5) -> None:
         self.batch, self.tokens, self.heads, self.head_dim, self.layers = 8, 750, 8, 128, 12
@@ -279,6 +282,15 @@ class Gemma4AudioAttention(Workload):
                     for _ in range(self.layers)]
         self.out = torch.empty(shape, device="cuda")
         self.attention = attention
+        self.torch = torch
+        self.unfused = False
+        blocks = -(-self.tokens // self.chunk)
+        context = self.chunk + self.past
+        query = torch.arange(blocks * self.chunk, device="cuda").view(blocks, self.chunk, 1)
+        key = (torch.arange(blocks, device="cuda") * self.chunk - self.past).view(blocks, 1, 1) + torch.arange(
+            context, device="cuda")
+        allowed = (query - key >= 0) & (query - key < self.past) & (key >= 0)
+        self.mask = ~(allowed & (key < self.lengths.view(-1, 1, 1, 1)))[:, None]
         self.launches = self.layers
         elements = self.batch * self.tokens * self.heads * self.head_dim
         per_layer = 4.0 * (4 * elements + self.rel_positions * self.heads * self.head_dim)
@@ -287,8 +299,33 @@ class Gemma4AudioAttention(Workload):
     def run(self) -> None:
         for layer in range(self.layers):
             q, k, v = self.qkv[layer]
+            if self.unfused:
+                self.out.copy_(self.reference_ops(q, k, v, self.rel[layer]))
+                continue
             self.attention.local_attention(q, k, v, self.rel[layer], self.lengths, chunk=self.chunk, past=self.past,
                                            future=0, softcap=50.0, invalid=-1e9, out=self.out)
+
+    def reference_ops(self, q, k, v, rel):
+        """The reference's sequence of ops (gemma4.py:256-282)."""
+        F = self.torch.nn.functional
+        batch, tokens, heads, dim = q.shape
+        chunk, past = self.chunk, self.past
+        context, blocks = chunk + past, self.mask.shape[2]
+
+        def contexts(x):
+            x = F.pad(x, (0, 0, 0, 0, past, chunk - 1))
+            return self.torch.movedim(x.unfold(1, context, chunk), -1, 2)
+
+        qb = F.pad(q, (0, 0, 0, 0, 0, blocks * chunk - tokens)).view(batch, blocks, chunk, heads, dim)
+        qb = qb.permute(0, 3, 1, 2, 4)
+        content = qb @ contexts(k).permute(0, 3, 1, 4, 2)
+        position = qb.reshape(batch, heads, -1, dim) @ rel.permute(1, 2, 0)
+        position = F.pad(position.view(batch, heads, blocks, chunk, -1), (0, context + 1 - rel.shape[0]))
+        position = position.view(batch, heads, blocks, chunk * (context + 1))[..., : chunk * context]
+        scores = self.torch.tanh((content + position.view(batch, heads, blocks, chunk, context)) / 50.0) * 50.0
+        weights = F.softmax(scores.masked_fill(self.mask, -1e9), dim=-1)
+        out = weights @ contexts(v).permute(0, 3, 1, 2, 4)
+        return out.permute(0, 2, 3, 1, 4).reshape(batch, blocks * chunk, heads, dim)[:, :tokens]
 
     def config(self) -> dict:
         return {"workload": self.name, "batch": self.batch, "tokens": self.tokens, "heads": self.heads,
@@ -743,6 +780,12 @@ def measure(torch, workload: Workload, steps: int, warmup: int) -> dict:
         result["module_ms_per_step"] = round(timed["module"], 4)
         result["module_unfused_ms_per_step"] = round(timed["module_unfused"], 4)
         result["module_speedup_vs_unfused"] = round(timed["module_unfused"] / timed["module"], 3)
+    if isinstance(workload, Gemma4AudioAttention):
+        workload.unfused = True
+        unfused = time_graph(torch, workload, steps, warmup)
+        workload.unfused = False
+        result["unfused_ms_per_step"] = round(unfused, 4)
+        result["speedup_vs_unfused"] = round(unfused / ms, 3)
     if isinstance(workload, Qwen3DecodeStepFused):
         workload.unfused = True
         unfused = time_graph(torch, workload, steps, min(warmup, workload.steps), reset=workload.reset)

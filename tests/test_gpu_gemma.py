@@ -57,8 +57,9 @@ def test_local_attention_matches_oracle(device, heads, head_dim, future):
     """Blocks of 12 audio tokens, each seeing itself and the 11 before it
     (Gemma 4 E2B/E4B's audio layers), ragged lengths including tokens past a
     sequence's end, relative keys of 13 distances, soft cap 50.  Head sizes
-    64-256 run on the kernel that takes runs of blocks (the last run reaching
-    past the final block); head_dim 40 on the one-wave-per-block kernel."""
+    64, 128 and 192 run on the matrix-core kernel that takes runs of blocks
+    (the last run reaching past the final block); head_dim 40 on the
+    one-wave-per-block kernel."""
     from asrback_amd import attention
 
     say("local attention", heads, head_dim, future)
