@@ -487,14 +487,36 @@ __global__ __launch_bounds__(HD) void decode_combine_kernel(const DecodeArgs a) 
   const int b = blockIdx.y;
   const int d = threadIdx.x;
   const int64_t idx0 = ((int64_t)b * p.heads_q + hq) * a.splits;
-  float mx = kNegInf;
-  for (int s = 0; s < a.splits; ++s) mx = fmaxf(mx, a.ws_ml[(idx0 + s) * 2]);
-  const float mxu = mx == kNegInf ? 0.f : mx;
   float lsum = 0.f, osum = 0.f;
-  for (int s = 0; s < a.splits; ++s) {
-    const float w = fast_exp2(a.ws_ml[(idx0 + s) * 2] - mxu);
-    lsum = fmaf(a.ws_ml[(idx0 + s) * 2 + 1], w, lsum);
-    osum = fmaf(a.ws_o[(idx0 + s) * HD + d], w, osum);
+  constexpr int kBatch = 8;  // splits whose partials are loaded in one round trip
+  if (a.splits <= kBatch) {
+    float m[kBatch], l[kBatch], o[kBatch];
+#pragma unroll
+    for (int s = 0; s < kBatch; ++s) {
+      const int t = min(s, a.splits - 1);  // surplus slots repeat the last split, weighted 0
+      m[s] = a.ws_ml[(idx0 + t) * 2];
+      l[s] = a.ws_ml[(idx0 + t) * 2 + 1];
+      o[s] = a.ws_o[(idx0 + t) * HD + d];
+    }
+    float mx = kNegInf;
+#pragma unroll
+    for (int s = 0; s < kBatch; ++s) mx = fmaxf(mx, m[s]);
+    const float mxu = mx == kNegInf ? 0.f : mx;
+#pragma unroll
+    for (int s = 0; s < kBatch; ++s) {
+      const float w = s < a.splits ? fast_exp2(m[s] - mxu) : 0.f;
+      lsum = fmaf(l[s], w, lsum);
+      osum = fmaf(o[s], w, osum);
+    }
+  } else {
+    float mx = kNegInf;
+    for (int s = 0; s < a.splits; ++s) mx = fmaxf(mx, a.ws_ml[(idx0 + s) * 2]);
+    const float mxu = mx == kNegInf ? 0.f : mx;
+    for (int s = 0; s < a.splits; ++s) {
+      const float w = fast_exp2(a.ws_ml[(idx0 + s) * 2] - mxu);
+      lsum = fmaf(a.ws_ml[(idx0 + s) * 2 + 1], w, lsum);
+      osum = fmaf(a.ws_o[(idx0 + s) * HD + d], w, osum);
+    }
   }
   T* op = static_cast<T*>(p.out) + (int64_t)b * p.o_batch_stride + (int64_t)hq * p.o_head_stride + d;
   Elem<T>::store1(op, lsum > 0.f ? osum / lsum : 0.f);
