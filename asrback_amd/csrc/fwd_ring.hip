@@ -183,15 +183,21 @@ __device__ __forceinline__ void work_item(const asrattn_fwd_params& p, int q_til
   b = bh / p.heads_q;
 }
 
-template <int HD, int RB, int KS, int BN, int ST>
+// DS > 1 splits the head dimensions over DS waves per row block (head_dim
+// 512, whose 32 rows of queries and outputs do not fit one wave's registers
+// without spilling): each takes HD / DS dimensions of the queries, keys and
+// outputs, the partial scores of a row block's waves are summed through LDS,
+// and every one of them runs the same softmax.
+template <int HD, int RB, int KS, int BN, int ST, int DS = 1>
 struct RingShape {
-  static constexpr int kW = RB * KS;                  // waves
+  static constexpr int kW = RB * KS * DS;             // waves
   static constexpr int kBM = 32 * RB;                 // query rows per workgroup
   static constexpr int kThreads = 64 * kW;
   static constexpr int kSpan = KS * BN;               // keys per ring stage
   static constexpr int kKB = BN / 32;                 // 32-key blocks per sub-tile
-  static constexpr int kKSteps = HD / 16;             // k-steps of S^T
-  static constexpr int kDB = HD / 32;                 // 32-row blocks of O^T
+  static constexpr int kDH = HD / DS;                 // head dimensions per wave
+  static constexpr int kKSteps = kDH / 16;            // k-steps of S^T
+  static constexpr int kDB = kDH / 32;                // 32-row blocks of O^T
   static constexpr int kRowBytes = HD * 2;
   static constexpr int kCPR = HD / 8;                 // 16-byte chunks per row
   static constexpr int kTileBytes = kSpan * kRowBytes;  // the K (or V) rows of a stage
@@ -205,32 +211,42 @@ struct RingShape {
   static constexpr int kMergeFloats = (kDB * 16 + 2) * 64;
   static constexpr int kMergeBytes = RB * (KS - 1) * kMergeFloats * 4;
   static constexpr int kRingBytes = ST * kStageBytes;
+  // Partial scores of the dimension splits (lane-major, per wave), after
+  // the ring.
+  static constexpr int kPartialBytes = DS > 1 ? kW * kKB * 16 * 64 * 4 : 0;
   static constexpr int kEpilogue = KS > 1 ? kMergeBytes : kOutBytes;
-  static constexpr int kLds = kRingBytes > kEpilogue ? kRingBytes : kEpilogue;
-  static_assert(HD == 64 || HD == 128, "head_dim");
+  static constexpr int kMain = kRingBytes + kPartialBytes;
+  static constexpr int kLds = kMain > kEpilogue ? kMain : kEpilogue;
+  static_assert(HD == 64 || HD == 128 || HD == 256 || HD == 512, "head_dim");
   static_assert(BN % 32 == 0 && kDmaPerTile % kW == 0 && kDmaPerWave >= 1, "tile / workgroup mapping");
   static_assert(ST >= 2 && ST <= 4, "ring depth");
   static_assert(KS == 1 || 32 * kOutRow * 2 <= kMergeFloats * 4, "output staging fits a merge slot");
+  static_assert(DS == 1 || (KS == 1 && kKSteps % 8 == 0), "dimension splits: one key split, whole 256-byte groups");
 };
 
-// Physical chunk of logical chunk c in row r of a K tile, and its inverse.
+// Physical chunk of logical chunk c in row r of a K tile, and its inverse;
+// rows of more than 16 chunks (head_dim 256, 512) rotate within each group
+// of 16 chunks.
 template <int HD>
 __device__ __forceinline__ int k_phys(int r, int c) {
-  return HD == 128 ? ((c + r) & 15) : ((c + (r >> 1)) & 7);
+  if constexpr (HD == 64) return (c + (r >> 1)) & 7;
+  return (c & ~15) | ((c + r) & 15);
 }
 template <int HD>
 __device__ __forceinline__ int k_logical(int r, int pc) {
-  return HD == 128 ? ((pc - r) & 15) : ((pc - (r >> 1)) & 7);
+  if constexpr (HD == 64) return (pc - (r >> 1)) & 7;
+  return (pc & ~15) | ((pc - r) & 15);
 }
 // V tiles: an XOR, its own inverse.
 template <int HD>
 __device__ __forceinline__ int v_phys(int r, int c) {
-  return HD == 128 ? (c ^ (4 * (r & 3))) : (c ^ (4 * ((r >> 1) & 1)));
+  return HD == 64 ? (c ^ (4 * ((r >> 1) & 1))) : (c ^ (4 * (r & 3)));
 }
 
-template <int HD, int RB, int KS, int BN, int ST, int OCC, int FS>
-__global__ __launch_bounds__(64 * RB * KS, OCC) void fwd_ring_kernel(const FwdArgs a, int q_tiles, int total) {
-  using S = RingShape<HD, RB, KS, BN, ST>;
+template <int HD, int RB, int KS, int BN, int ST, int OCC, int FS, bool WIN, int DS>
+__global__ __launch_bounds__(64 * RB * KS * DS, OCC) void fwd_ring_kernel(const FwdArgs a, int q_tiles, int total) {
+  using S = RingShape<HD, RB, KS, BN, ST, DS>;
+  constexpr int DH = S::kDH;
   constexpr int BM = S::kBM, KST = S::kKSteps, DB = S::kDB, KB = S::kKB, RBYTES = S::kRowBytes;
   constexpr int CPR = S::kCPR, NPW = S::kDmaPerWave, SB = S::kStageBytes, TB = S::kTileBytes;
   constexpr int SPAN = S::kSpan;
@@ -266,18 +282,26 @@ __global__ __launch_bounds__(64 * RB * KS, OCC) void fwd_ring_kernel(const FwdAr
 
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: DMA destinations live in SGPRs
-  const int rb = wave % RB;  // row block
-  const int ks = wave / RB;  // key split
+  const int rb = wave % RB;         // row block
+  const int ks = (wave / RB) % KS;  // key split
+  const int dh = wave / (RB * KS);  // dimension split: head dims [dh DH, dh DH + DH)
   const int r32 = lane & 31;
   const int half = lane >> 5;
   const int wrow0 = row0 + 32 * rb;
   const int row = wrow0 + r32;
   const bool row_ok = row < sv.len_q;
-  const int row_lim = visible_keys(p, sv, row);
-  // Keys the workgroup (its last row) and this wave (its last row) see.
-  const int kend = visible_keys(p, sv, min(row0 + BM, sv.len_q) - 1);
-  const int wkend = wrow0 < sv.len_q ? visible_keys(p, sv, min(wrow0 + 32, sv.len_q) - 1) : 0;
-  const int n_tiles = (kend + SPAN - 1) / SPAN;
+  // Keys the workgroup (its last row) and this wave (its last row) see; with
+  // a sliding window they start at the workgroup's first row's first key,
+  // kofs, and the tiles count keys from there.
+  const int last = min(row0 + BM, sv.len_q) - 1;
+  const int wlast = min(wrow0 + 32, sv.len_q) - 1;
+  const int kend = visible_keys(p, sv, last);
+  const int kofs = WIN ? min(first_key(p, sv, row0), kend) : 0;
+  const int n_tiles = (kend - kofs + SPAN - 1) / SPAN;
+  const int row_lim = visible_keys(p, sv, row) - kofs;  // this row: keys [row_lo, row_lim) after kofs
+  const int row_lo = WIN ? first_key(p, sv, row) - kofs : 0;
+  const int wkend = wrow0 < sv.len_q ? visible_keys(p, sv, wlast) - kofs : 0;
+  const int wkbeg = WIN && wrow0 < sv.len_q ? first_key(p, sv, wrow0) - kofs : 0;
 
   // Low 32 bits of the flat address of an LDS variable are its LDS offset.
   const uint32_t lds_base = (uint32_t)(uintptr_t)lds;
@@ -286,7 +310,7 @@ __global__ __launch_bounds__(64 * RB * KS, OCC) void fwd_ring_kernel(const FwdAr
   bf16x8_t qreg[KST];
   {
     const bf16_raw* qp = static_cast<const bf16_raw*>(p.q) + sv.q_off +
-                         (int64_t)(row_ok ? row : 0) * p.q_token_stride + half * 8;
+                         (int64_t)(row_ok ? row : 0) * p.q_token_stride + dh * DH + half * 8;
 #pragma unroll
     for (int kk = 0; kk < KST; ++kk) {
       const uint4 v = row_ok ? *reinterpret_cast<const uint4*>(qp + kk * 16) : make_uint4(0, 0, 0, 0);
@@ -297,10 +321,10 @@ __global__ __launch_bounds__(64 * RB * KS, OCC) void fwd_ring_kernel(const FwdAr
   // K/V of the (sequence, kv head) up to the workgroup's last visible key.
   const uint32_t kts = (uint32_t)(p.k_token_stride * 2);
   const uint32_t vts = (uint32_t)(p.v_token_stride * 2);
-  const __amdgpu_buffer_rsrc_t krs =
-      buffer_rsrc(static_cast<const bf16_raw*>(p.k) + sv.k_off, (uint32_t)kend * kts);
-  const __amdgpu_buffer_rsrc_t vrs =
-      buffer_rsrc(static_cast<const bf16_raw*>(p.v) + sv.v_off, (uint32_t)kend * vts);
+  const __amdgpu_buffer_rsrc_t krs = buffer_rsrc(
+      static_cast<const bf16_raw*>(p.k) + sv.k_off + (int64_t)kofs * p.k_token_stride, (uint32_t)(kend - kofs) * kts);
+  const __amdgpu_buffer_rsrc_t vrs = buffer_rsrc(
+      static_cast<const bf16_raw*>(p.v) + sv.v_off + (int64_t)kofs * p.v_token_stride, (uint32_t)(kend - kofs) * vts);
 
   // DMA instruction wave * NPW + i of a tile fills LDS slots 64 j + lane:
   // physical row s / CPR, physical chunk s % CPR, holding the logical chunk
@@ -336,18 +360,24 @@ __global__ __launch_bounds__(64 * RB * KS, OCC) void fwd_ring_kernel(const FwdAr
   // are masked to 18 bits (LDS addresses), which proves their sign bit
   // clear: only then do the constant parts added below (stage, key block,
   // k-step) fold into the ds_read offset field.
-  uint32_t kaddr[KST];
+  // Past 16 chunks the rotation repeats in every 256-byte group, so k-step
+  // kk reads at kaddr[kk % 8] + 256 (kk / 8) (and V column block db at
+  // vaddr[db % 4] + 256 (db / 4)).
+  constexpr int KA = KST < 8 ? KST : 8;
+  constexpr int VA = DB < 4 ? DB : 4;
+  uint32_t kaddr[KA];
 #pragma unroll
-  for (int kk = 0; kk < KST; ++kk)
-    kaddr[kk] = (lds_base + (uint32_t)(ks * BN + r32) * RBYTES + (uint32_t)k_phys<HD>(r32, 2 * kk + half) * 16) &
+  for (int kk = 0; kk < KA; ++kk)
+    kaddr[kk] = (lds_base + (uint32_t)(ks * BN + r32) * RBYTES +
+                 (uint32_t)k_phys<HD>(r32, 2 * (dh * KST + kk) + half) * 16) &
                 0x3ffffu;
   const int tr_row = 4 * ((lane >> 4) >> 1) + ((lane & 15) >> 2);
   const int tr_cc = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);  // chunk within the 32-column block
-  uint32_t vaddr[DB];
+  uint32_t vaddr[VA];
 #pragma unroll
-  for (int db = 0; db < DB; ++db)
+  for (int db = 0; db < VA; ++db)
     vaddr[db] = (lds_base + TB + (uint32_t)(ks * BN + tr_row) * RBYTES +
-                 (uint32_t)v_phys<HD>(tr_row, 4 * db + tr_cc) * 16 + (lane & 1) * 8) &
+                 (uint32_t)v_phys<HD>(tr_row, 4 * (dh * DB + db) + tr_cc) * 16 + (lane & 1) * 8) &
                 0x3ffffu;
 
   f32x16_t oacc[DB];
@@ -363,10 +393,12 @@ __global__ __launch_bounds__(64 * RB * KS, OCC) void fwd_ring_kernel(const FwdAr
   float l_run = 0.f;
 
   // Whether the sub-tile starting at key kt needs the per-key mask (some row
-  // of the wave sees fewer than all of its keys; the wave's first row sees
-  // the fewest).
-  const int wmin = wrow0 < sv.len_q ? visible_keys(p, sv, wrow0) : 0;
-  auto masked = [&](int kt) { return kt + BN > wmin; };
+  // of the wave sees fewer than all of its keys -- the wave's first row sees
+  // the fewest -- or, with a window, some row's window starts inside it --
+  // the wave's last row's starts latest).
+  const int wmin = wrow0 < sv.len_q ? visible_keys(p, sv, wrow0) - kofs : 0;
+  const int wlo = WIN && wrow0 < sv.len_q ? first_key(p, sv, wlast) - kofs : 0;
+  auto masked = [&](int kt) { return kt + BN > wmin || (WIN && kt < wlo); };
 
   // S^T of tile j (stage stage_idx) into s.
   auto qk = [&](int stage_idx, f32x16_t* s) {
@@ -376,18 +408,19 @@ __global__ __launch_bounds__(64 * RB * KS, OCC) void fwd_ring_kernel(const FwdAr
 #pragma unroll
     for (int kk = 0; kk < KST; ++kk) {
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb) s[kb] = mfma32(lds_read16(kaddr[kk] + so + kb * 32 * RBYTES), qreg[kk], s[kb]);
+      for (int kb = 0; kb < KB; ++kb)
+        s[kb] = mfma32(lds_read16(kaddr[kk % KA] + (kk / KA) * 256 + so + kb * 32 * RBYTES), qreg[kk], s[kb]);
     }
   };
-  // Keys at or past the row's limit -> -inf.  Accumulator r of block kb is
-  // key kt + 32 kb + 8 (r / 4) + 4 half + r % 4.
+  // Keys outside the row's [row_lo, row_lim) -> -inf.  Accumulator r of
+  // block kb is key kt + 32 kb + 8 (r / 4) + 4 half + r % 4.
   auto mask = [&](int kt, f32x16_t* s) {
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int key = kt + kb * 32 + (r / 4) * 8 + half * 4 + (r % 4);
-        if (key >= row_lim) s[kb][r] = kNegInf;
+        if (key >= row_lim || (WIN && key < row_lo)) s[kb][r] = kNegInf;
       }
   };
   // Row max over the tile, combined across the half waves, scaled.
@@ -425,8 +458,9 @@ __global__ __launch_bounds__(64 * RB * KS, OCC) void fwd_ring_kernel(const FwdAr
     for (int t = 0; t < 2 * KB; ++t) {
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
-        const short4_t lo = ds_read_tr(vaddr[db] + so + 16 * t * RBYTES);
-        const short4_t hi = ds_read_tr(vaddr[db] + so + (16 * t + 8) * RBYTES);
+        const uint32_t va = vaddr[db % VA] + (db / VA) * 256 + so;
+        const short4_t lo = ds_read_tr(va + 16 * t * RBYTES);
+        const short4_t hi = ds_read_tr(va + (16 * t + 8) * RBYTES);
         const bf16x8_t av = __builtin_bit_cast(bf16x8_t, (short8_t){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
         oacc[db] = mfma32(av, pb[t], oacc[db]);
       }
@@ -450,11 +484,32 @@ __global__ __launch_bounds__(64 * RB * KS, OCC) void fwd_ring_kernel(const FwdAr
     wait_dma<2 * NPW, ST - 2>(min(ST - 2, n_tiles - 1 - j));
     __syncthreads();
     if (j + ST - 1 < n_tiles) issue(j + ST - 1, (stage_idx + ST - 1) % ST);
-    const int kt = j * SPAN + ks * BN;  // this wave's first key
-    if (kt >= wkend) return;  // uniform per wave; the barrier is above
-
+    const int kt = j * SPAN + ks * BN;  // this wave's first key (after kofs)
+    const bool idle = kt >= wkend || (WIN && kt + BN <= wkbeg);  // uniform per wave
     f32x16_t s[KB];
-    qk(stage_idx, s);
+    if constexpr (DS > 1) {
+      // Every wave reaches the partial-score barrier, idle or not.
+      float* const part = reinterpret_cast<float*>(lds + S::kRingBytes);
+      if (!idle) {
+        qk(stage_idx, s);
+        float* mine = part + (size_t)wave * KB * 16 * 64 + lane;
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) mine[(kb * 16 + r) * 64] = s[kb][r];
+      }
+      __syncthreads();
+      if (idle) return;
+      const int partner = rb + RB * (1 - dh);  // DS == 2
+      const float* other = part + (size_t)partner * KB * 16 * 64 + lane;
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[kb][r] += other[(kb * 16 + r) * 64];
+    } else {
+      if (idle) return;  // the barrier is above
+      qk(stage_idx, s);
+    }
     if (masked(kt)) mask(kt, s);
     const float mt = rowmax(s);
     // Rescale only when some row's max grew past the slack (always on the
@@ -533,19 +588,19 @@ __global__ __launch_bounds__(64 * RB * KS, OCC) void fwd_ring_kernel(const FwdAr
     for (int i = 0; i < 4; ++i) {
       const uint32_t w0 = pack_bf16x2(oacc[db][4 * i] * inv, oacc[db][4 * i + 1] * inv);
       const uint32_t w1 = pack_bf16x2(oacc[db][4 * i + 2] * inv, oacc[db][4 * i + 3] * inv);
-      *reinterpret_cast<uint2*>(stage + r32 * ORS + db * 32 + i * 8 + half * 4) = make_uint2(w0, w1);
+      *reinterpret_cast<uint2*>(stage + r32 * ORS + dh * DH + db * 32 + i * 8 + half * 4) = make_uint2(w0, w1);
     }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   // ... and store them to global memory 16 bytes per lane, whole rows per
   // instruction.
-  constexpr int kRowChunks = HD / 8;
+  constexpr int kRowChunks = DH / 8;  // this wave's columns
 #pragma unroll
   for (int i = 0; i < 32 * kRowChunks / 64; ++i) {
     const int ch = i * 64 + lane;
     const int r = ch / kRowChunks;
-    const int col = (ch % kRowChunks) * 8;
+    const int col = dh * DH + (ch % kRowChunks) * 8;
     const int orow = wrow0 + r;
     const uint4 val = *reinterpret_cast<const uint4*>(stage + r * ORS + col);
     if (orow < sv.len_q) {
@@ -555,9 +610,9 @@ __global__ __launch_bounds__(64 * RB * KS, OCC) void fwd_ring_kernel(const FwdAr
   }
 }
 
-template <int HD, int RB, int KS, int BN, int ST, int OCC, int FS>
+template <int HD, int RB, int KS, int BN, int ST, int OCC, int FS, bool WIN = false, int DS = 1>
 hipError_t launch_typed(const FwdArgs& a, hipStream_t stream) {
-  using S = RingShape<HD, RB, KS, BN, ST>;
+  using S = RingShape<HD, RB, KS, BN, ST, DS>;
   const asrattn_fwd_params& p = a.p;
   const int q_tiles = (p.max_len_q + S::kBM - 1) / S::kBM;
   const long long total = (long long)q_tiles * p.heads_q * p.batch;
@@ -566,7 +621,7 @@ hipError_t launch_typed(const FwdArgs& a, hipStream_t stream) {
   const int copies = FS > 0 ? 2 : 1;
   if (copies * total > 0x7fffffffLL) return hipErrorInvalidConfiguration;
   const unsigned grid = (unsigned)(copies * total);
-  hipLaunchKernelGGL((fwd_ring_kernel<HD, RB, KS, BN, ST, OCC, FS>), dim3(grid), dim3(S::kThreads), 0, stream, a,
+  hipLaunchKernelGGL((fwd_ring_kernel<HD, RB, KS, BN, ST, OCC, FS, WIN, DS>), dim3(grid), dim3(S::kThreads), 0, stream, a,
                      q_tiles, (int)total);
   return hipGetLastError();
 }
@@ -577,15 +632,31 @@ hipError_t launch_hd(const FwdArgs& a, hipStream_t stream) {
   // two workgroups per CU, whose waves pair up on the SIMDs without sharing
   // a barrier.  Key splits (KS > 1) halve the rows a CU holds at two waves
   // per SIMD, which costs more than they save once the batch fills the GPU.
-  if (a.f.memory != nullptr) return launch_typed<HD, 4, 1, 64, 2, 2, kFsmnFusedKernel>(a, stream);
-  return launch_typed<HD, 4, 1, 64, 2, 2, 0>(a, stream);
+  // Head dims 256 and 512 (Gemma 4) hold 32 rows' queries and outputs in
+  // one wave's registers only at one wave per SIMD; their tiles fill 128 KB
+  // of LDS in two stages (64 keys at 256, 32 at 512).
+  // Sliding windows (causal, Gemma 4) take a variant that starts each
+  // workgroup's keys at its first row's window.
+  const bool win = a.p.window > 0;
+  if constexpr (HD == 512) {
+    // 64 query rows, each row block's dimensions over two waves.
+    if (win) return launch_typed<HD, 2, 1, 32, 2, 1, 0, true, 2>(a, stream);
+    return launch_typed<HD, 2, 1, 32, 2, 1, 0, false, 2>(a, stream);
+  } else if constexpr (HD == 256) {
+    if (win) return launch_typed<HD, 4, 1, 64, 2, 1, 0, true>(a, stream);
+    return launch_typed<HD, 4, 1, 64, 2, 1, 0>(a, stream);
+  } else {
+    if (win) return launch_typed<HD, 4, 1, 64, 2, 2, 0, true>(a, stream);
+    if (a.f.memory != nullptr) return launch_typed<HD, 4, 1, 64, 2, 2, kFsmnFusedKernel>(a, stream);
+    return launch_typed<HD, 4, 1, 64, 2, 2, 0>(a, stream);
+  }
 }
 
 }  // namespace
 
 bool fwd_ring_supported(const asrattn_fwd_params& p) {
-  if (p.dtype != ASRATTN_BF16 || (p.head_dim != 64 && p.head_dim != 128)) return false;
-  if (p.window > 0) return false;  // sliding windows run on the vector-ALU kernel
+  if (p.dtype != ASRATTN_BF16) return false;
+  if (p.head_dim != 64 && p.head_dim != 128 && p.head_dim != 256 && p.head_dim != 512) return false;
   // A key row must end before the next one starts for the resource bound
   // (last visible key's row end) to cover every visible key.
   if (p.k_token_stride < p.head_dim || p.v_token_stride < p.head_dim) return false;
@@ -601,7 +672,12 @@ hipError_t launch_fwd_ring(const asrattn_fwd_params& p, const FsmnArgs* fsmn, hi
   a.p = p;
   a.c = p.scale * kLog2e;
   a.f = fsmn != nullptr ? *fsmn : FsmnArgs{};
-  return p.head_dim == 64 ? launch_hd<64>(a, stream) : launch_hd<128>(a, stream);
+  switch (p.head_dim) {
+    case 64: return launch_hd<64>(a, stream);
+    case 128: return launch_hd<128>(a, stream);
+    case 256: return launch_hd<256>(a, stream);
+    default: return launch_hd<512>(a, stream);
+  }
 }
 
 }  // namespace asrattn

@@ -23,8 +23,8 @@ layers over a 512-key window at head_dim 256, full layers at 512).
 ``secondary`` adds the SenseVoice attention with its FSMN memory fused into
 the same launch (timed beside the reference's ops for both outputs), Whisper
 large-v3-turbo's encoder attention (20 heads x 64, 1500 frames, batch 16, 32
-layers), Qwen3's causal grouped-query prompt pass and Gemma 4's blocked
-local audio attention.
+layers), Qwen3's causal grouped-query prompt pass, Gemma 4's blocked local
+audio attention and Gemma 4's windowed prompt pass.
 
 ``cpu_baseline`` times the CPU restatement of the reference's attention
 (torch SDPA with the key-padding mask, float32, the reference's CPU path) on
@@ -331,6 +331,62 @@ class Gemma4AudioAttention(Workload):
         return {"workload": self.name, "batch": self.batch, "tokens": self.tokens, "heads": self.heads,
                 "head_dim": self.head_dim, "layers": self.layers, "chunk": self.chunk, "past": self.past,
                 "dtype": "float32"}
+
+
+class Gemma4Prefill(Workload):
+    """Gemma 4's prompt pass (gemma4.py:534-561, ``scale=1.0``) with
+    transformers' ``Gemma4TextConfig`` defaults, as the reference admits
+    windows: 8 padded prompts (``PREFILL_ROWS``, gemma4.py:66) of 800 +
+    U{0..40} tokens, 8 query heads over 4 kv heads, causal; sliding layers
+    head_dim 256 within a 512-key window, full layers head_dim 512; 30
+    layers, five sliding to one full.  Value: TFLOP/s over each valid
+    query's visible keys, ``4 * head_dim * 8`` per (query, key)."""
+
+    name = "gemma4-prefill-attention"
+    unit = "TFLOP/s"
+    bound = "mfma"
+    kernel = "fwd_ring_kernel"
+
+    def __init__(self, torch, attention, seed: int = 7) -> None:
+        rng = np.random.default_rng(seed)
+        self.batch, self.heads_q, self.heads_kv, self.layers, self.window = 8, 8, 4, 30, 512
+        self.full = [(i + 1) % 6 == 0 for i in range(self.layers)]
+        sizes = (800 + rng.integers(0, 41, size=self.batch)).astype(np.int64)
+        self.length = int(sizes.max())
+        self.sizes = torch.from_numpy(sizes.astype(np.int32)).cuda()
+        g = torch.Generator(device="cuda").manual_seed(seed)
+        self.q, self.kv = [], []
+        for full in self.full:
+            hd = 512 if full else 256
+            self.q.append(torch.randn((self.batch, self.length, self.heads_q, hd), generator=g, device="cuda",
+                                      dtype=torch.bfloat16))
+            self.kv.append(torch.randn((2, self.batch, self.length, self.heads_kv, hd), generator=g, device="cuda",
+                                       dtype=torch.bfloat16))
+        self.out = {hd: torch.empty((self.batch, self.length, self.heads_q, hd), device="cuda", dtype=torch.bfloat16)
+                    for hd in (256, 512)}
+        self.attention = attention
+        self.launches = self.layers
+        work = 0.0
+        for full in self.full:
+            hd = 512 if full else 256
+            for n in sizes:
+                visible = np.arange(1, int(n) + 1)
+                keys = visible.sum() if full else np.minimum(visible, self.window).sum()
+                work += 4.0 * hd * self.heads_q * float(keys)
+        self.work_per_step = work
+
+    def run(self) -> None:
+        for layer, full in enumerate(self.full):
+            k, v = self.kv[layer]
+            hd = k.shape[-1]
+            self.attention.flash(self.q[layer], k, v, causal=1, seqused_k=self.sizes, scale=1.0,
+                                 window=None if full else self.window, out=self.out[hd])
+
+    def config(self) -> dict:
+        return {"workload": self.name, "prompts": self.batch, "prompt_tokens": "800 + U{0..40}",
+                "heads_q": self.heads_q, "heads_kv": self.heads_kv,
+                "head_dim": "256 (sliding, window 512) / 512 (full)", "layers": self.layers,
+                "full_layers": sum(self.full), "causal": "top-left"}
 
 
 class Gemma4TextDecode(Workload):
@@ -897,7 +953,7 @@ def main() -> int:
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--only", choices=["sensevoice", "sensevoice-fsmn", "turbo", "qwen3", "qwen3-paged",
                                            "qwen3-fused", "qwen3-prefill", "whisper-small", "choice",
-                                           "gemma4-audio", "gemma4-decode", "copy"],
+                                           "gemma4-audio", "gemma4-decode", "gemma4-prefill", "copy"],
                         default=None,
                         help="measure one workload only (for profiling)")
     parser.add_argument("--sweep", action="store_true",
@@ -933,6 +989,7 @@ def main() -> int:
         "qwen3-prefill": Qwen3Prefill,
         "gemma4-audio": Gemma4AudioAttention,
         "gemma4-decode": Gemma4TextDecode,
+        "gemma4-prefill": Gemma4Prefill,
         "choice": GreedyChoice,
         "whisper-small": WhisperSmallDecoderStep,
         "copy": CopyCalibration,
@@ -954,7 +1011,7 @@ def main() -> int:
         decode.append(measure(torch, cls(torch, attention), args.steps, args.warmup))
         torch.cuda.empty_cache()
     secondary = []
-    for cls in (SenseVoiceAttentionFsmn, WhisperTurboEncoder, Qwen3Prefill, Gemma4AudioAttention):
+    for cls in (SenseVoiceAttentionFsmn, WhisperTurboEncoder, Qwen3Prefill, Gemma4AudioAttention, Gemma4Prefill):
         log(f"bench: {cls.name}")
         secondary.append(measure(torch, cls(torch, attention), args.steps, args.warmup))
         torch.cuda.empty_cache()

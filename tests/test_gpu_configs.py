@@ -553,13 +553,17 @@ def test_gemma_decode_window_and_head_sizes(ops, device, dtype, hd, heads_q, hea
         (torch.float32, 256, 8, 2, 512),
         (torch.float32, 512, 8, 1, 100),
         (torch.bfloat16, 128, 16, 8, 100),
+        (torch.bfloat16, 512, 8, 2, 100),
+        (torch.bfloat16, 64, 8, 8, 33),
     ],
 )
 def test_gemma_prefill_window_and_head_sizes(ops, device, dtype, hd, heads_q, heads_kv, window):
     """Gemma 4's padded prompt pass (gemma4.py:552-559, masks :1227-1235):
     causal, keys before each prompt's size, the sliding window, scale 1.0,
     grouped-query attention, head_dim 256/512, against the oracle's masked
-    SDPA on the prompts' own rows."""
+    SDPA on the prompts' own rows.  bf16 runs on the matrix-core kernel
+    (head_dim 512 with its dimensions split over two waves), float32 on the
+    vector-ALU kernel."""
     say("gemma prefill", dtype, hd, heads_q, heads_kv, window)
     batch, length = 3, 700
     sizes = torch.tensor([700, 513, 37])
