@@ -23,8 +23,9 @@ layers over a 512-key window at head_dim 256, full layers at 512).
 ``secondary`` adds the SenseVoice attention with its FSMN memory fused into
 the same launch (timed beside the reference's ops for both outputs), Whisper
 large-v3-turbo's encoder attention (20 heads x 64, 1500 frames, batch 16, 32
-layers), Qwen3's causal grouped-query prompt pass, Gemma 4's blocked local
-audio attention and Gemma 4's windowed prompt pass.
+layers), Qwen3's causal grouped-query prompt pass and its audio encoder's
+windowed attention, Gemma 4's blocked local audio attention and Gemma 4's
+windowed prompt pass.
 
 ``cpu_baseline`` times the CPU restatement of the reference's attention
 (torch SDPA with the key-padding mask, float32, the reference's CPU path) on
@@ -251,6 +252,46 @@ class Qwen3Prefill(Workload):
     def config(self) -> dict:
         return {"workload": self.name, "prompts": 8, "prompt_tokens": "390 + U{10..40}", "heads_q": self.heads_q,
                 "heads_kv": self.heads_kv, "head_dim": self.head_dim, "layers": self.layers, "causal": "bottom-right"}
+
+
+class Qwen3AudioAttention(Workload):
+    """Qwen3-ASR's audio encoder attention (qwen3_asr.py:216-221 over the
+    windows of :303-310) with transformers' ``Qwen3ASRAudioEncoderConfig``
+    defaults: 16 heads x 64, 24 layers, chunks of 13 tokens in attention
+    windows of 8 chunks (104 tokens); 8 audio windows of 30 s (390 tokens:
+    segments of 104, 104, 104, 78), packed, non-causal.  Value: TFLOP/s over
+    each segment's queries x keys."""
+
+    name = "qwen3-asr-audio-encoder-attention"
+    unit = "TFLOP/s"
+    bound = "mfma"
+    kernel = "fwd_ring_kernel"
+
+    def __init__(self, torch, attention, seed: int = 8) -> None:
+        self.heads, self.head_dim, self.layers, self.windows = 16, 64, 24, 8
+        segments = [104, 104, 104, 78] * self.windows
+        tokens = sum(segments)
+        self.cu = torch.from_numpy(np.concatenate(([0], np.cumsum(segments))).astype(np.int32)).cuda()
+        self.longest = max(segments)
+        g = torch.Generator(device="cuda").manual_seed(seed)
+        width = self.heads * self.head_dim
+        self.qkv = [torch.randn((tokens, 3 * width), generator=g, device="cuda", dtype=torch.bfloat16)
+                    for _ in range(self.layers)]
+        self.attention = attention
+        self.launches = self.layers
+        self.work_per_step = float(sum(4 * n * n * width for n in segments)) * self.layers
+        self.segments = len(segments)
+
+    def run(self) -> None:
+        width = self.heads * self.head_dim
+        for layer in range(self.layers):
+            q, k, v = (t.view(-1, self.heads, self.head_dim) for t in self.qkv[layer].split(width, dim=-1))
+            self.attention.varlen_attn(q, k, v, self.cu, self.cu, self.longest, self.longest)
+
+    def config(self) -> dict:
+        return {"workload": self.name, "windows": self.windows, "segments": self.segments,
+                "segment_tokens": "104, 104, 104, 78 per 30 s window", "heads": self.heads,
+                "head_dim": self.head_dim, "layers": self.layers}
 
 
 class Gemma4AudioAttention(Workload):
@@ -953,7 +994,7 @@ def main() -> int:
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--only", choices=["sensevoice", "sensevoice-fsmn", "turbo", "qwen3", "qwen3-paged",
                                            "qwen3-fused", "qwen3-prefill", "whisper-small", "choice",
-                                           "gemma4-audio", "gemma4-decode", "gemma4-prefill", "copy"],
+                                           "qwen3-audio", "gemma4-audio", "gemma4-decode", "gemma4-prefill", "copy"],
                         default=None,
                         help="measure one workload only (for profiling)")
     parser.add_argument("--sweep", action="store_true",
@@ -987,6 +1028,7 @@ def main() -> int:
         "qwen3-paged": Qwen3DecodePaged,
         "qwen3-fused": Qwen3DecodeStepFused,
         "qwen3-prefill": Qwen3Prefill,
+        "qwen3-audio": Qwen3AudioAttention,
         "gemma4-audio": Gemma4AudioAttention,
         "gemma4-decode": Gemma4TextDecode,
         "gemma4-prefill": Gemma4Prefill,
@@ -1011,7 +1053,8 @@ def main() -> int:
         decode.append(measure(torch, cls(torch, attention), args.steps, args.warmup))
         torch.cuda.empty_cache()
     secondary = []
-    for cls in (SenseVoiceAttentionFsmn, WhisperTurboEncoder, Qwen3Prefill, Gemma4AudioAttention, Gemma4Prefill):
+    for cls in (SenseVoiceAttentionFsmn, WhisperTurboEncoder, Qwen3Prefill, Qwen3AudioAttention, Gemma4AudioAttention,
+                Gemma4Prefill):
         log(f"bench: {cls.name}")
         secondary.append(measure(torch, cls(torch, attention), args.steps, args.warmup))
         torch.cuda.empty_cache()
