@@ -807,6 +807,13 @@ TRAFFIC_KEYS = {
     "sensevoice-small-encoder-attention": "sensevoice",
     "qwen3-asr-1.7b-decode-attention": "qwen3",
     "whisper-small-decoder-step-attention": "whisper-small",
+    "whisper-large-v3-turbo-encoder-attention": "turbo",
+    "qwen3-asr-1.7b-decode-attention-paged": "qwen3-paged",
+    "qwen3-asr-1.7b-prefill-attention": "qwen3-prefill",
+    "qwen3-asr-audio-encoder-attention": "qwen3-audio",
+    "gemma4-audio-local-attention": "gemma4-audio",
+    "gemma4-text-decode-attention": "gemma4-decode",
+    "gemma4-prefill-attention": "gemma4-prefill",
 }
 
 
