@@ -155,25 +155,28 @@ __device__ __forceinline__ int ranked_sequence(const asrattn_fwd_params& p, int 
 // Launch id -> (sequence, query head, query tile).  Dispatch hands ids out
 // in order as workgroup slots free up, round-robin over the 8 XCDs.  With
 // per-sequence key counts (ragged batches of at most 64 sequences) the
-// (sequence, head) pairs are taken in decreasing key count -- the longest
-// work starts first and short pairs fill in behind it -- and pair P goes to
-// XCD P % 8 with its query tiles consecutive there, so its K/V stay in one
-// L2.  The second half of each XCD's items runs in increasing key count:
-// when the grid fills two slots per CU, the longest items then share a CU
-// with the shortest (3% on the SenseVoice batch).  Otherwise ids are
-// remapped so that each XCD gets a contiguous range of items (the same L2
-// grouping).
+// (sequence, kv head) units are taken in decreasing key count -- the
+// longest work starts first and short units fill in behind it -- and unit U
+// goes to XCD U % 8 with all its items consecutive there (every query head
+// sharing the kv head, every query tile), so its K/V stay in one L2.  The
+// second half of each XCD's items runs in increasing key count: when the
+// grid fills two slots per CU, the longest items then share a CU with the
+// shortest (3% on the SenseVoice batch).  Otherwise ids are remapped so that
+// each XCD gets a contiguous range of items (the same L2 grouping).
 __device__ __forceinline__ void work_item(const asrattn_fwd_params& p, int q_tiles, int total, int id, int& b,
                                           int& hq, int& qt) {
   const bool ragged = p.seqused_k != nullptr || p.cu_seqlens_k != nullptr;
-  if (ragged && p.batch <= 64 && (p.batch * p.heads_q) % 8 == 0) {
+  if (ragged && p.batch <= 64 && (p.batch * p.heads_kv) % 8 == 0) {
+    const int group = p.heads_q / p.heads_kv;
+    const int per_unit = group * q_tiles;
     const int per = total / 8, half = per / 2;
     int k = id >> 3;
     if (k >= half) k = per - 1 - (k - half);
-    const int pair = (k / q_tiles) * 8 + (id & 7);
-    qt = k % q_tiles;
-    hq = pair % p.heads_q;
-    b = ranked_sequence(p, pair / p.heads_q);
+    const int unit = (k / per_unit) * 8 + (id & 7);
+    const int w = k % per_unit;
+    qt = w % q_tiles;
+    hq = (unit % p.heads_kv) * group + w / q_tiles;
+    b = ranked_sequence(p, unit / p.heads_kv);
     return;
   }
   const int item = xcd_remap(id, total);
