@@ -110,3 +110,22 @@ def test_bench_refuses_more_than_one_gpu():
     )
     assert result.returncode == 2
     assert "one GPU" in result.stderr
+
+
+def test_bench_gemma_audio_reference_ops_match_oracle():
+    """The Gemma 4 audio line times the reference's sequence of ops as its
+    unfused baseline; on the CPU that sequence equals the oracle's blocked
+    attention (pad, unfold, relative shift, soft cap, mask, softmax)."""
+    import types
+
+    import bench
+    from oracle import gemma4 as og
+
+    torch.manual_seed(0)
+    lengths = torch.tensor([50, 23])
+    w = types.SimpleNamespace(torch=torch, chunk=12, past=12, mask=og.blocked_mask(lengths, 50, 12, 12, 0))
+    q, k, v = (torch.randn(2, 50, 2, 16) for _ in range(3))
+    rel = torch.randn(13, 2, 16)
+    got = bench.Gemma4AudioAttention.reference_ops(w, q, k, v, rel)
+    ref = og.local_attention(q, k, v, rel, w.mask, 12, 12, 0, 50.0, -1e9)
+    assert torch.equal(got, ref)
