@@ -6,9 +6,9 @@
 // partial dot products of a row's lanes are summed with DPP.  Key/value
 // tiles of BN rows are staged in LDS as fp32 and read by all lanes at the
 // same address (broadcast, no bank conflicts).  This is the fp32 path
-// (Whisper in float32, the reference's CPU/fp32 dtype), the exact-arithmetic
-// twin of the bf16 matrix-core kernel, and the kernel for head sizes the
-// matrix-core kernel does not hold in registers (Gemma 4's 256 and 512).
+// (Whisper in float32, the reference's CPU/fp32 dtype; Gemma 4 in float32 at
+// head_dim 256 and 512) and the exact-arithmetic twin of the bf16
+// matrix-core kernel.
 #include "common.hpp"
 #include "fwd_common.hpp"
 #include "kernels.hpp"

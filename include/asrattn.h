@@ -72,8 +72,8 @@ enum asrattn_causal {
  * stride is ignored and the sequence has cu_seqlens_q[b+1] - cu_seqlens_q[b]
  * queries (at most max_len_q).  seqused_k (int32[batch], device, optional)
  * caps the keys sequence b uses.  A query with no visible key gets zeros.
- * head_dim 64 or 128, and 256 or 512 on the vector-ALU kernel (Gemma 4's
- * sliding and full layers, gemma4.py:552-559, scale 1.0).
+ * head_dim 64, 128, 256 or 512 (256 and 512: Gemma 4's sliding and full
+ * layers, gemma4.py:552-559, scale 1.0).
  *
  * Replaces:
  *   F.scaled_dot_product_attention   src/asrback/models/whisper.py:102-104
