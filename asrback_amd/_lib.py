@@ -19,7 +19,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must be imported before the library; see above)
 
 LIBRARY = Path(__file__).resolve().with_name("libasrattn.so")
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 # enum asrattn_status / asrattn_dtype / asrattn_causal
 OK = 0
@@ -124,6 +124,7 @@ class AppendParams(ctypes.Structure):
         ("cos", _ptr),
         ("sin", _ptr),
         ("rope_batch_stride", _i64),
+        ("v_norm", _i32),
     ]
 
 

@@ -478,6 +478,7 @@ def decode_append(
     workspace: Tensor | None = None,
     pages: PageTable | None = None,
     window: int | None = None,
+    v_norm: bool = False,
 ) -> Tensor:
     """A decoder step with its prologue fused in (``asrattn_decode_append``;
     with ``pages``, ``k``/``v`` are page pools as for :func:`decode`):
@@ -490,6 +491,8 @@ def decode_append(
     attends keys ``0 .. positions[b]``.  Replaces the step path of
     ``TextAttention._project`` and ``step`` (``qwen3_asr.py:366-372``,
     ``:409-432``) and Whisper's cache scatter (``whisper.py:224-228``).
+    ``v_norm``: ``v_new`` also gets the RMS norm, without weights, before it
+    is written and used (Gemma 4, ``gemma4.py:515``, ``:522-532``).
     Returns ``(batch, heads_q, head_dim)``."""
     if q.dim() != 3 or k.dim() != 4 or v.shape != k.shape:
         raise ValueError(
@@ -544,6 +547,7 @@ def decode_append(
     app.eps = eps
     app.cos, app.sin = _ptr(cos), _ptr(sin)
     app.rope_batch_stride = 0 if cos is None else cos.stride(0)
+    app.v_norm = 1 if v_norm else 0
     lib = _lib.load()
     need = lib.asrattn_decode_workspace_size(ctypes.byref(params))
     if workspace is None and need and need != ctypes.c_size_t(-1).value:

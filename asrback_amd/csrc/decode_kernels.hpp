@@ -167,6 +167,23 @@ __device__ __forceinline__ uint4 norm_rotate(uint4 raw, bool has_norm, const uin
   return pack<T>(x);
 }
 
+// RMS norm without weights (x / sqrt(mean(x^2) + eps), float32 sums,
+// rounded once to T).
+template <typename T, int HD, int LPK>
+__device__ __forceinline__ uint4 rms_unweighted(uint4 raw, float eps) {
+  constexpr int EPL = Elem<T>::kPerVec;
+  float x[EPL];
+  unpack<T>(raw, x);
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) ss = fmaf(x[e], x[e], ss);
+  ss = group_sum<LPK>(ss);
+  const float r = rsqrtf(ss * (1.f / HD) + eps);
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) x[e] = round_to<T>(x[e] * r);
+  return pack<T>(x);
+}
+
 // Online-softmax state of one stream for the G query heads of a kv head.
 template <typename T, int HD, int G, int W>
 struct Stream {
@@ -318,6 +335,7 @@ __global__ __launch_bounds__(64 * W, (DecodeShape<T, HD, G, W>::kOcc)) void deco
   // arithmetic runs after that batch is issued.
   const asrattn_append_params& ap = a.ap;
   const bool has_norm = APPEND && ap.q_norm != nullptr;
+  const bool has_vnorm = APPEND && ap.v_norm != 0;
   const bool has_rot = APPEND && ap.cos != nullptr;
   uint4 knew = {}, vnew = {}, qw = {}, kw = {}, cs = {}, sn = {};
   if constexpr (APPEND) {
@@ -402,6 +420,7 @@ __global__ __launch_bounds__(64 * W, (DecodeShape<T, HD, G, W>::kOcc)) void deco
 #pragma unroll
     for (int g = 0; g < G; ++g) st.q[g] = norm_rotate<T, HD, LPK>(st.q[g], has_norm, qw, has_rot, cs, sn, ap.eps, sub);
     knew = norm_rotate<T, HD, LPK>(knew, has_norm, kw, has_rot, cs, sn, ap.eps, sub);
+    if (has_vnorm) vnew = rms_unweighted<T, HD, LPK>(vnew, ap.eps);
     st.seed(knew, vnew, split == a.splits - 1 && stream == 0);
   }
   for (int base = k0; base < k1; base += 2 * STEP) {

@@ -30,7 +30,7 @@ import torch.nn.functional as F
 from torch import Tensor, nn
 
 from . import _lib
-from .attention import KeyPrefix, decode, decode_supported, flash, local_attention
+from .attention import KeyPrefix, decode, decode_append, decode_supported, flash, local_attention
 
 
 class RMSNorm(nn.Module):
@@ -245,6 +245,15 @@ class TextAttention(nn.Module):
         the step's (causal at ``positions``, the window on sliding layers, as
         ``TextModel.step`` builds it from the same positions)."""
         del mask  # keys 0 .. position, and the window: from positions
+        if not self.shared and decode_supported(x.dtype, self.head_dim, self.heads // self.kv_heads):
+            # One launch: the q/k/v norms, the rotation, the cache writes at
+            # each row's position and the attention (asrattn_decode_append).
+            q, k, v = self.qkv_proj(x).split(self.sizes, dim=-1)
+            shape = (len(x), -1, self.head_dim)
+            output = decode_append(q.view(shape), k.view(shape), v.view(shape), cache.keys, cache.values, positions,
+                                   q_norm=self.q_norm.weight, k_norm=self.k_norm.weight, eps=self.q_norm.eps,
+                                   cos=cos, sin=sin, scale=1.0, window=self.window, v_norm=True)
+            return self.o_proj(output.reshape(len(x), -1))
         q, k, v = self._project(x, cos, sin)
         if not self.shared:
             rows = torch.arange(len(x), device=x.device)

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define ASRATTN_ABI_VERSION 7
+#define ASRATTN_ABI_VERSION 8
 
 enum asrattn_status {
   ASRATTN_OK = 0,
@@ -223,7 +223,8 @@ int asrattn_decode(const asrattn_decode_params* params, void* workspace,
  *
  *   q'  = rot(norm(q[b, h, :], q_norm), cos[b], sin[b])
  *   k'  = rot(norm(k_new[b, h', :], k_norm), cos[b], sin[b])
- *   k[b, p, h', :] = k',  v[b, p, h', :] = v_new[b, h', :]   (if p < max_len_k)
+ *   v'  = norm(v_new[b, h', :], 1)                 (v_norm != 0; else v_new)
+ *   k[b, p, h', :] = k',  v[b, p, h', :] = v'      (if p < max_len_k)
  *   out[b, h, :] = attention of q' over cache keys j < min(p, max_len_k)
  *                  and the new key/value
  *
@@ -243,6 +244,9 @@ int asrattn_decode(const asrattn_decode_params* params, void* workspace,
  *       attention                    src/asrback/models/qwen3_asr.py:409-432
  *   keys.scatter_/values.scatter_ of the Whisper step (no norm, no
  *       rotation)                    src/asrback/models/whisper.py:224-228
+ *   q_norm/k_norm/v_norm + rotate and the cache writes of Gemma 4's step
+ *                                    src/asrback/models/gemma4.py:522-532,
+ *                                    :563-587
  */
 typedef struct asrattn_append_params {
   const void* k_new; /* (batch, heads_kv, head_dim), before norm and rotation */
@@ -255,6 +259,8 @@ typedef struct asrattn_append_params {
   const void* cos; /* (batch, head_dim) tables at each row's position, or NULL */
   const void* sin; /* NULL exactly when cos is */
   int64_t rope_batch_stride;
+  int32_t v_norm; /* nonzero: RMS-normalize the new value, without weights
+                     (Gemma 4's v_norm, gemma4.py:515) */
 } asrattn_append_params;
 
 int asrattn_decode_append(const asrattn_decode_params* params, const asrattn_append_params* append,

@@ -392,6 +392,54 @@ def test_decode_append_matches_oracle(ops, device, dtype, batch, heads_q, heads_
     assert torch.equal(kd.cpu()[untouched], keys[untouched]) and torch.equal(vd.cpu()[untouched], values[untouched])
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_decode_append_gemma_prologue_matches_oracle(ops, device, dtype):
+    """Gemma 4's step prologue fused into the decode launch (gemma4.py:515,
+    :522-532, :563-587): q/k norms with weights, the value norm without
+    (v_norm), the rotation, the cache writes, then 8 query heads over 4 kv
+    heads at head_dim 256 over a 512-key window, scale 1.0; against the
+    oracle module's norms (oracle.gemma4) and SDPA with the step's mask."""
+    from oracle import gemma4 as og
+
+    say("decode append gemma", dtype)
+    hd, length, eps, window = 256, 1280, 1e-6, 512
+    batch, heads_q, heads_kv = 5, 8, 4
+    positions = torch.tensor([0, 37, 511, 512, 1000], dtype=torch.int64)
+    q = randn(batch, heads_q, hd, seed=71, dtype=dtype)
+    k_new = randn(batch, heads_kv, hd, seed=72, dtype=dtype)
+    v_new = randn(batch, heads_kv, hd, seed=73, dtype=dtype)
+    keys = randn(batch, length, heads_kv, hd, seed=74, dtype=dtype)
+    values = randn(batch, length, heads_kv, hd, seed=75, dtype=dtype)
+    g = torch.Generator().manual_seed(76)
+    q_norm, k_norm, v_norm = og._Norm(hd, eps), og._Norm(hd, eps), og._Norm(hd, eps, scale=False)
+    with torch.no_grad():
+        q_norm.weight.copy_(torch.rand(hd, generator=g) + 0.5)
+        k_norm.weight.copy_(torch.rand(hd, generator=g) + 0.5)
+    q_w, k_w = q_norm.weight.detach().to(dtype), k_norm.weight.detach().to(dtype)
+    q_norm.weight.data, k_norm.weight.data = q_w.float(), k_w.float()
+    cos, sin = oa.rope_tables(1e4, hd, length, dtype)
+    cos, sin = cos[positions], sin[positions]
+    with torch.no_grad():
+        qn = og.rotate(q_norm(q), cos, sin)
+        kn = og.rotate(k_norm(k_new), cos, sin)
+        vn = v_norm(v_new)
+    rows = torch.arange(batch)
+    keys_ref, values_ref = keys.clone(), values.clone()
+    keys_ref[rows, positions] = kn
+    values_ref[rows, positions] = vn
+    mask = oa.gemma_step_mask(positions, length, window)
+    ref = oa.sdpa(qn.float().view(batch, heads_kv, -1, hd), keys_ref.float().transpose(1, 2),
+                  values_ref.float().transpose(1, 2), attn_mask=mask, scale=1.0).reshape(batch, heads_q, hd)
+
+    kd, vd = keys.to(device), values.to(device)
+    out = ops.decode_append(q.to(device), k_new.to(device), v_new.to(device), kd, vd, positions.to(device),
+                            q_norm=q_w.to(device), k_norm=k_w.to(device), eps=eps, cos=cos.to(device),
+                            sin=sin.to(device), scale=1.0, window=window, v_norm=True)
+    assert max_rel_err(out, ref) < TOL[dtype]
+    assert _ulp_diff_ok(kd.cpu()[rows, positions], kn, dtype)
+    assert _ulp_diff_ok(vd.cpu()[rows, positions], vn, dtype)
+
+
 def _paginate(cache_k, cache_v, needed, page_size, seed, spare=3):
     """Pools ``(num_pages, page_size, H, D)`` holding each slab row's first
     ``needed[b]`` positions in randomly placed pages, and the block table

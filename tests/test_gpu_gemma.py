@@ -134,7 +134,10 @@ def test_text_attention_prefill_and_steps_match_oracle(device, layer_type, dtype
     then decoder steps at each row's own position (gemma4.py:534-587): q/k/v
     norms, rotary embedding, no scaling, 8 query heads over 1 kv head,
     head_dim 256 with a 24-key window (sliding) or 512 (full); and a KV-shared
-    layer reading the same cache and prompt keys."""
+    layer reading the same cache and prompt keys.  Steps of layers with their
+    own keys run the fused prologue (norms, rotation and cache writes in the
+    decode launch) where the decode kernel takes the head size; the cache
+    holds what the oracle's holds."""
     from asrback_amd import gemma4 as ag
 
     say("gemma text attention", layer_type, dtype)
@@ -182,3 +185,4 @@ def test_text_attention_prefill_and_steps_match_oracle(device, layer_type, dtype
         assert max_rel_err(out_shared.float().cpu(), expected_shared) < tol
         positions += 1
     assert max_rel_err(cache.keys.float().cpu(), keys.float()) < (1e-5 if dtype == torch.float32 else 1e-2)
+    assert max_rel_err(cache.values.float().cpu(), values.float()) < (1e-5 if dtype == torch.float32 else 1e-2)
