@@ -19,7 +19,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must be imported before the library; see above)
 
 LIBRARY = Path(__file__).resolve().with_name("libasrattn.so")
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 # enum asrattn_status / asrattn_dtype / asrattn_causal
 OK = 0
@@ -200,8 +200,9 @@ SIGNATURES = {
     "asrattn_local": (ctypes.c_int, [ctypes.POINTER(LocalParams), _ptr]),
     "asrattn_choose": (
         ctypes.c_int,
-        [_ptr, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, _ptr, _ptr, _ptr, _ptr],
+        [_ptr, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, _ptr, _ptr, _ptr, _ptr, ctypes.c_size_t, _ptr],
     ),
+    "asrattn_choose_workspace_size": (ctypes.c_size_t, [ctypes.c_int64, ctypes.c_int64]),
     "asrattn_decode_workspace_size": (ctypes.c_size_t, [ctypes.POINTER(DecodeParams)]),
     "asrattn_decode_num_splits": (ctypes.c_int, [ctypes.POINTER(DecodeParams)]),
     "asrattn_last_error": (ctypes.c_char_p, []),

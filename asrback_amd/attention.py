@@ -627,7 +627,9 @@ def greedy_choice(logits: Tensor, suppress: Tensor | None = None) -> tuple[Tenso
     uint8 ``(vocab,)``) to -inf, and ``log_softmax`` at it.  Replaces the
     greedy path of ``whisper.py:962-974`` and ``qwen3_asr.py:1200-1210``;
     ``logits`` is not modified.  Returns int64 tokens and float32
-    log-probabilities ``(rows,)``."""
+    log-probabilities ``(rows,)``.  Rows are split over several workgroups
+    through the device's decode workspace (a fixed address, so a captured
+    graph replays it)."""
     if logits.dim() != 2 or logits.dtype != torch.float32:
         raise ValueError("greedy_choice takes float32 (rows, vocab) logits")
     if logits.stride(-1) != 1:
@@ -643,9 +645,12 @@ def greedy_choice(logits: Tensor, suppress: Tensor | None = None) -> tuple[Tenso
     token = torch.empty(rows, dtype=torch.int64, device=device)
     logprob = torch.empty(rows, dtype=torch.float32, device=device)
     lib = _lib.load()
+    need = lib.asrattn_choose_workspace_size(rows, vocab)
+    workspace = decode_workspace(need, device) if need else None
+    size = 0 if workspace is None else workspace.numel() * workspace.element_size()
     _lib.check(
         lib.asrattn_choose(logits.data_ptr(), rows, vocab, logits.stride(0), _ptr(suppress), token.data_ptr(),
-                           logprob.data_ptr(), _stream(device)),
+                           logprob.data_ptr(), _ptr(workspace), size, _stream(device)),
         "asrattn_choose",
     )
     return token, logprob

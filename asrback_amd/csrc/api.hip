@@ -311,8 +311,13 @@ int asrattn_decode(const asrattn_decode_params* params, void* workspace, size_t 
   return run_decode(params, nullptr, nullptr, workspace, workspace_bytes, stream, "asrattn_decode");
 }
 
+size_t asrattn_choose_workspace_size(int64_t rows, int64_t vocab) {
+  if (rows <= 0 || rows > 0x7fffffffLL || vocab < 1 || vocab >= (1LL << 29)) return 0;
+  return asrattn::choose_workspace_bytes(rows, vocab);
+}
+
 int asrattn_choose(const float* logits, int64_t rows, int64_t vocab, int64_t row_stride, const uint8_t* suppress,
-                   int64_t* token, float* logprob, void* stream) {
+                   int64_t* token, float* logprob, void* workspace, size_t workspace_bytes, void* stream) {
   if (rows < 0 || rows > 0x7fffffffLL) return fail(ASRATTN_ERR_INVALID, "rows (%lld) out of range", (long long)rows);
   // Rows are addressed with 32-bit byte offsets.
   if (vocab < 1 || vocab >= (1LL << 29)) return fail(ASRATTN_ERR_INVALID, "vocab (%lld) out of range", (long long)vocab);
@@ -320,7 +325,15 @@ int asrattn_choose(const float* logits, int64_t rows, int64_t vocab, int64_t row
   if (rows == 0) return ok();
   if (logits == nullptr || token == nullptr || logprob == nullptr)
     return fail(ASRATTN_ERR_INVALID, "logits, token and logprob must be non-NULL");
-  return from_hip(asrattn::launch_choose(logits, rows, vocab, row_stride, suppress, token, logprob,
+  if (workspace != nullptr) {
+    const size_t need = asrattn::choose_workspace_bytes(rows, vocab);
+    if (workspace_bytes < need)
+      return fail(ASRATTN_ERR_WORKSPACE, "choose workspace of %zu bytes, %zu needed", workspace_bytes, need);
+    if (need == 0) workspace = nullptr;
+  } else if (workspace_bytes != 0) {
+    return fail(ASRATTN_ERR_INVALID, "workspace_bytes without a workspace");
+  }
+  return from_hip(asrattn::launch_choose(logits, rows, vocab, row_stride, suppress, token, logprob, workspace,
                                          static_cast<hipStream_t>(stream)),
                   "asrattn_choose");
 }

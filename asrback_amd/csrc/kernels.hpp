@@ -32,8 +32,13 @@ bool fwd_ring_supported(const asrattn_fwd_params& p);
 
 // Greedy choice per row of fp32 logits: argmax (first index on ties) and its
 // log-probability; suppress (uint8 per vocabulary entry) may be null.
+// Splits per row of the two-launch choice (1: one workgroup per row).
+int choose_splits(int64_t rows, int64_t vocab);
+// Workspace bytes of the split form (0 when one workgroup per row is used).
+size_t choose_workspace_bytes(int64_t rows, int64_t vocab);
+// workspace: at least choose_workspace_bytes, or null for one workgroup per row.
 hipError_t launch_choose(const float* logits, int64_t rows, int64_t vocab, int64_t row_stride, const uint8_t* suppress,
-                         int64_t* token, float* logprob, hipStream_t stream);
+                         int64_t* token, float* logprob, void* workspace, hipStream_t stream);
 
 // Multi-row forward on the vector ALUs (fp32 or bf16, head_dim 64 or 128):
 // the fp32 path, the fallback for bf16 layouts the matrix-core kernel does

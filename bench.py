@@ -654,9 +654,13 @@ class Qwen3DecodeStepFused(Qwen3Decode):
 class GreedyChoice(Workload):
     """The greedy token choice of a Qwen3-ASR-1.7B decoder step
     (qwen3_asr.py:1200-1210): argmax and log_softmax at it over fp32 logits
-    (64, 151936), one fused pass; ``unfused_ms_per_step`` times torch's
-    argmax, log_softmax and gather on the same logits.  Bytes: the logits
-    read once, tokens and log-probabilities written."""
+    (64, 151936): each row read by 32 workgroups, their partials folded
+    by a second launch; ``unfused_ms_per_step`` times torch's argmax,
+    log_softmax and gather on the same logits.  A step is the choices of
+    eight decoder steps over eight logits buffers (311 MB, more than the
+    Infinity Cache), so that one graph replay is not just its own launch
+    overhead.  Bytes: the logits read once, tokens and log-probabilities
+    written."""
 
     name = "qwen3-asr-1.7b-greedy-choice"
     unit = "GB/s"
@@ -665,28 +669,26 @@ class GreedyChoice(Workload):
 
     def __init__(self, torch, attention, seed: int = 5) -> None:
         self.torch = torch
-        self.rows, self.vocab = 64, 151936
+        self.rows, self.vocab, self.steps = 64, 151936, 8
         g = torch.Generator(device="cuda").manual_seed(seed)
-        self.logits = torch.randn((self.rows, self.vocab), generator=g, device="cuda") * 4
-        self.token = torch.empty(self.rows, dtype=torch.long, device="cuda")
-        self.logprob = torch.empty(self.rows, device="cuda")
+        self.logits = [torch.randn((self.rows, self.vocab), generator=g, device="cuda") * 4 for _ in range(self.steps)]
         self.attention = attention
-        self.launches = 1
-        self.work_per_step = float(self.rows * self.vocab * 4 + self.rows * 12)
+        self.launches = self.steps
+        self.work_per_step = float(self.steps * (self.rows * self.vocab * 4 + self.rows * 12))
         self.unfused = False
 
     def run(self) -> None:
         torch = self.torch
-        if not self.unfused:
-            token, logprob = self.attention.greedy_choice(self.logits)
-        else:
-            token = self.logits.argmax(dim=-1)
-            logprob = torch.log_softmax(self.logits, dim=-1).gather(1, token[:, None]).squeeze(1)
-        self.token.copy_(token)
-        self.logprob.copy_(logprob)
+        for logits in self.logits:
+            if not self.unfused:
+                self.token, self.logprob = self.attention.greedy_choice(logits)
+            else:
+                self.token = logits.argmax(dim=-1)
+                self.logprob = torch.log_softmax(logits, dim=-1).gather(1, self.token[:, None]).squeeze(1)
 
     def config(self) -> dict:
-        return {"workload": self.name, "rows": self.rows, "vocab": self.vocab, "dtype": "float32 logits"}
+        return {"workload": self.name, "rows": self.rows, "vocab": self.vocab, "dtype": "float32 logits",
+                "choices_per_step": self.steps}
 
 
 class WhisperSmallDecoderStep(Workload):

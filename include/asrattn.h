@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define ASRATTN_ABI_VERSION 8
+#define ASRATTN_ABI_VERSION 9
 
 enum asrattn_status {
   ASRATTN_OK = 0,
@@ -303,7 +303,7 @@ int asrattn_decode_paged(const asrattn_decode_params* params, const asrattn_appe
                          const asrattn_paged_kv* paged, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
- * Greedy next token per row of float32 logits, in one pass:
+ * Greedy next token per row of float32 logits:
  *
  *   token[r]   = argmax_j x[r, j]       (first index among equal maxima)
  *   logprob[r] = log_softmax(x[r])[token[r]] = -log(sum_j exp(x[r, j] - max))
@@ -315,13 +315,23 @@ int asrattn_decode_paged(const asrattn_decode_params* params, const asrattn_appe
  * r*row_stride (row_stride >= vocab); token is int64[rows], logprob
  * float32[rows].  1 <= vocab < 2^29.
  *
+ * With a workspace of asrattn_choose_workspace_size(rows, vocab) bytes
+ * (caller-owned device memory, a fixed address for graphs; 0 means none is
+ * needed) each row is read by several workgroups and a second launch folds
+ * their partial maxima and sums; without one (NULL, 0) one workgroup per
+ * row reads it in a single launch.  A workspace smaller than the size
+ * returns ASRATTN_ERR_WORKSPACE.  Results are the same either way.
+ *
  * Replaces the greedy path of:
  *   logits.masked_fill_(suppress, -inf); argmax; log_softmax; gather
  *                                    src/asrback/models/whisper.py:962-974
  *   argmax; log_softmax; gather      src/asrback/models/qwen3_asr.py:1200-1210
  */
 int asrattn_choose(const float* logits, int64_t rows, int64_t vocab, int64_t row_stride, const uint8_t* suppress,
-                   int64_t* token, float* logprob, void* stream);
+                   int64_t* token, float* logprob, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace bytes asrattn_choose uses to split rows (0: it does not). */
+size_t asrattn_choose_workspace_size(int64_t rows, int64_t vocab);
 
 /*
  * Blocked local attention with relative position scores, in float32 (Gemma 4's

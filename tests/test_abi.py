@@ -44,6 +44,7 @@ def test_header_declares_expected_entry_points():
         "asrattn_decode_paged",
         "asrattn_local",
         "asrattn_choose",
+        "asrattn_choose_workspace_size",
         "asrattn_decode_workspace_size",
         "asrattn_decode_num_splits",
         "asrattn_last_error",
@@ -306,3 +307,19 @@ def test_workspace_size_and_split_choice(lib):
     p.num_splits = 4
     p.q = p.k = p.v = p.out = 16
     assert lib.asrattn_decode(ctypes.byref(p), None, 0, None) == _lib.ERR_WORKSPACE
+
+
+def test_choose_workspace_size_and_errors(lib):
+    """Qwen3's (64, 151936) logits split each row over 32 workgroups
+    (one 16-byte partial each); small vocabularies need no workspace; a
+    short workspace is an error, not a fault."""
+    from asrback_amd import _lib
+
+    assert lib.asrattn_choose_workspace_size(64, 151936) == 64 * 32 * 16
+    assert lib.asrattn_choose_workspace_size(4, 2000) == 0
+    assert lib.asrattn_choose_workspace_size(0, 151936) == 0
+    fake = 64  # never dereferenced: the checks come first
+    status = lib.asrattn_choose(fake, 64, 151936, 151936, None, fake, fake, fake, 16, None)
+    assert status == _lib.ERR_WORKSPACE
+    assert b"workspace" in lib.asrattn_last_error()
+    assert lib.asrattn_choose(fake, 64, 151936, 151936, None, fake, fake, None, 16, None) == _lib.ERR_INVALID
