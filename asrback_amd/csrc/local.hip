@@ -5,10 +5,11 @@
 // the output once.
 //
 // local_mfma_kernel (head_dim 64, 128 or 192, blocks of at most 16
-// queries over at most 32 context slots): a workgroup takes a run of
-// consecutive blocks of one (sequence, head), one wave per block.  The run's
-// values (each serves two blocks) and the head's relative keys are staged
-// in LDS, the queries and keys go straight to registers; each wave computes
+// queries over at most 32 context slots): a workgroup walks runs of
+// consecutive blocks of one (sequence, head), one wave per block, loading
+// the next run's operands while the current one computes.  A run's values
+// (each serves two blocks) and the head's relative keys are staged in LDS,
+// the queries and keys go straight to registers; each wave computes
 // its block's scores, relative terms and weighted values as fp32 matrix
 // products on the matrix cores
 // (v_mfma_f32_16x16x4_f32, fp32 operands and accumulation), transposed as
@@ -18,6 +19,8 @@
 //
 // local_kernel (any other shape): one wave per (block, head, sequence),
 // one (query, slot) score per lane.
+#include <algorithm>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -48,16 +51,24 @@ size_t mfma_lds_floats(const asrattn_local_params& p, int nblk) {
 // Staging copies in flight per thread (16-byte loads issued before their
 // LDS stores).
 constexpr int kStageBatch = 8;
+// Relative-key copies per thread issued ahead of the first run's loads
+// (every chunk at head_dim up to 192 with four waves).
+constexpr int kRelBatch = 3;
 
 template <int KS>  // head_dim / 4: k-steps of a product over the head dimensions
-__global__ __launch_bounds__(64 * kMfmaMaxWaves) void local_mfma_kernel(const asrattn_local_params p, int nblk) {
+__global__ __launch_bounds__(64 * kMfmaMaxWaves, 2) void local_mfma_kernel(const asrattn_local_params p, int nblk,
+                                                                            int rpw) {
   extern __shared__ float smem[];
   constexpr int D = 4 * KS, RS = D + 4;
+  constexpr bool kPrefetch = KS <= 32;
   const int C = p.chunk, ctx = p.chunk + p.past + p.future, R = p.rel_positions;
   const int h = blockIdx.y;
   const int b = blockIdx.z;
-  const int u0 = blockIdx.x * nblk;  // the run's first block
-  const int key0 = u0 * C - p.past;  // key of staged row 0
+  const int runs = ((p.tokens + C - 1) / C + nblk - 1) / nblk;
+  // The workgroup's runs: r0 .. r1 - 1 (one at head_dim 192, which has no
+  // registers for the next run's operands).
+  const int r0 = blockIdx.x * rpw;
+  const int r1 = kPrefetch ? min(runs, r0 + rpw) : r0 + 1;
   const int rows = nblk * C + p.past + p.future;
   const int n = min(max(p.lengths[b], 0), p.tokens);  // valid keys of the sequence
   const int tid = threadIdx.x;
@@ -65,13 +76,12 @@ __global__ __launch_bounds__(64 * kMfmaMaxWaves) void local_mfma_kernel(const as
   float* Rs = Vs + rows * RS;  // [16][RS]
   float* Xs = Rs + 16 * RS;    // [wave][16][17]
 
-  // Lane (col, m): query column col of the wave's block, head dimensions
-  // [m KS, m KS + KS) -- the k slot m of every product step.
+  // Lane (col, m): query column col of the wave's block; k slot m of
+  // product step 4 j + e is head dimension 16 j + 4 m + e (any order of the
+  // dimensions over the k slots gives the same sums), so a row's operands
+  // are 16-byte loads of which four lanes cover 64 contiguous bytes.
   const int lane = tid & 63, wave = tid >> 6;
   const int col = lane & 15, m = lane >> 4;
-  const int u = u0 + wave;
-  const int query = u * C + col;
-  const bool qok = col < C && query < p.tokens;
   // Every row goes through a buffer resource that ends at the sequence's
   // last token, so tokens outside [0, tokens) read as zeros (the reference's
   // padding; offsets of negative keys wrap past the end) with no branch.
@@ -85,141 +95,196 @@ __global__ __launch_bounds__(64 * kMfmaMaxWaves) void local_mfma_kernel(const as
       buffer_rsrc(p.v + (int64_t)b * p.v_batch_stride + (int64_t)h * p.v_head_stride, (uint32_t)p.tokens * vts);
   const __amdgpu_buffer_rsrc_t rrs = buffer_rsrc(p.rel + (int64_t)h * p.rel_head_stride, (uint32_t)R * rps);
 
-  // The block's query col and the keys of context slots col and 16 + col,
-  // straight into the product operands.  Query columns past the block and
-  // slots past the context read nothing (an offset past every range; their
-  // results are never stored or are dropped from the softmax below).
+  // The query col of the wave's block in run `run` and the keys of context
+  // slots col and 16 + col, straight into the product operands.  Query
+  // columns past the block and slots past the context read nothing (an
+  // offset past every range; their results are never stored or are dropped
+  // from the softmax below).
   float qv[KS], kv[2][KS];
-  {
+  auto load_qk = [&](int run) {
     constexpr uint32_t kNowhere = 0x80000000u;  // past any range (ranges stay below 2^31)
-    const uint32_t dim0 = (uint32_t)m * KS * 4;
-    const uint32_t qo = col < C ? (uint32_t)query * qts + dim0 : kNowhere;
+    const int u = run * nblk + wave;
+    const uint32_t dim0 = (uint32_t)m * 16;
+    const uint32_t qo = col < C ? (uint32_t)(u * C + col) * qts + dim0 : kNowhere;
     const int key = u * C - p.past + col;
     const uint32_t ko0 = col < ctx ? (uint32_t)key * kts + dim0 : kNowhere;
     const uint32_t ko1 = 16 + col < ctx ? (uint32_t)(key + 16) * kts + dim0 : kNowhere;
 #pragma unroll
     for (int d = 0; d < KS; d += 4) {
-      const float4 t = __builtin_bit_cast(float4, buffer_load16(qrs, qo + d * 4));
-      const float4 k0 = __builtin_bit_cast(float4, buffer_load16(krs, ko0 + d * 4));
-      const float4 k1 = __builtin_bit_cast(float4, buffer_load16(krs, ko1 + d * 4));
+      const float4 t = __builtin_bit_cast(float4, buffer_load16(qrs, qo + d * 16));
+      const float4 k0 = __builtin_bit_cast(float4, buffer_load16(krs, ko0 + d * 16));
+      const float4 k1 = __builtin_bit_cast(float4, buffer_load16(krs, ko1 + d * 16));
       qv[d] = t.x, qv[d + 1] = t.y, qv[d + 2] = t.z, qv[d + 3] = t.w;
       kv[0][d] = k0.x, kv[0][d + 1] = k0.y, kv[0][d + 2] = k0.z, kv[0][d + 3] = k0.w;
       kv[1][d] = k1.x, kv[1][d + 1] = k1.y, kv[1][d + 2] = k1.z, kv[1][d + 3] = k1.w;
     }
-  }
+  };
 
-  // Staged value row r holds key key0 + r, then 16 relative rows (zeros
-  // past R).  Loads go out in batches ahead of their stores; the last
-  // batch's surplus threads repeat the last chunk (same value, same place).
+  // Staged value row r of run `run` holds key run nblk C - past + r.  Loads
+  // go out in batches ahead of their stores; the last batch's surplus
+  // threads repeat the last chunk (same value, same place).
   const int vchunks = rows * KS;
-  for (int base = tid; base < vchunks; base += kStageBatch * (int)blockDim.x) {
-    float4 x[kStageBatch];
+  const int vstride = kStageBatch * (int)blockDim.x;
+  float4 x[kStageBatch];
+  auto load_v = [&](int run, int base) {
+    const int key0 = run * nblk * C - p.past;
 #pragma unroll
     for (int j = 0; j < kStageBatch; ++j) {
       const int i = min(base + j * (int)blockDim.x, vchunks - 1);
       x[j] = __builtin_bit_cast(float4, buffer_load16(vrs, (uint32_t)(key0 + i / KS) * vts + (uint32_t)(i % KS) * 16));
     }
+  };
+  auto store_v = [&](int base) {
 #pragma unroll
     for (int j = 0; j < kStageBatch; ++j) {
       const int i = min(base + j * (int)blockDim.x, vchunks - 1);
       *reinterpret_cast<float4*>(Vs + (i / KS) * RS + (i % KS) * 4) = x[j];
     }
+  };
+  // The first batch comes from loads issued earlier (x); the rest load here.
+  auto stage_rest = [&](int run) {
+    store_v(tid);
+    for (int base = tid + vstride; base < vchunks; base += vstride) {
+      load_v(run, base);
+      store_v(base);
+    }
+  };
+
+  // The head's relative keys (16 rows, zeros past R) serve every run.  Their
+  // loads go out first, so that storing them waits for nothing else; the
+  // first run's queries and keys follow, then its values, which are only
+  // needed after its scores.
+  const int rchunks = 16 * KS;
+  float4 rl[kRelBatch];
+#pragma unroll
+  for (int j = 0; j < kRelBatch; ++j) {
+    const int i = min(tid + j * (int)blockDim.x, rchunks - 1);
+    rl[j] = __builtin_bit_cast(float4, buffer_load16(rrs, (uint32_t)(i / KS) * rps + (uint32_t)(i % KS) * 16));
   }
-  for (int i = tid; i < 16 * KS; i += blockDim.x)
+  load_qk(r0);
+  load_v(r0, tid);
+#pragma unroll
+  for (int j = 0; j < kRelBatch; ++j) {
+    const int i = min(tid + j * (int)blockDim.x, rchunks - 1);
+    *reinterpret_cast<float4*>(Rs + (i / KS) * RS + (i % KS) * 4) = rl[j];
+  }
+  for (int i = tid + kRelBatch * (int)blockDim.x; i < rchunks; i += blockDim.x)
     *reinterpret_cast<float4*>(Rs + (i / KS) * RS + (i % KS) * 4) =
         __builtin_bit_cast(float4, buffer_load16(rrs, (uint32_t)(i / KS) * rps + (uint32_t)(i % KS) * 16));
   __syncthreads();
 
-  // S^T: context slot 16 nt + col against query column col.
-  f32x4_t st[2];
-#pragma unroll
-  for (int nt = 0; nt < 2; ++nt) {
-    st[nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int d = 0; d < KS; ++d) st[nt] = mfma16(kv[nt][d], qv[d], st[nt]);
-  }
-  // Relative scores R^T[row][query]; lane holds rows 4 m + r of column col.
-  f32x4_t rt = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  {
-    const float* rr = Rs + col * RS + m * KS;
-#pragma unroll
-    for (int d = 0; d < KS; d += 4) {
-      const float4 rv = *reinterpret_cast<const float4*>(rr + d);
-      rt = mfma16(rv.x, qv[d], rt);
-      rt = mfma16(rv.y, qv[d + 1], rt);
-      rt = mfma16(rv.z, qv[d + 2], rt);
-      rt = mfma16(rv.w, qv[d + 3], rt);
-    }
-  }
-  // The reference's relative shift: slot t of query c adds relative row
-  // t - c when 0 <= t - c < R; rows move between lanes through LDS.
-  float* xs = Xs + wave * 16 * 17;
-#pragma unroll
-  for (int r = 0; r < 4; ++r) xs[col * 17 + 4 * m + r] = rt[r];
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-  // Soft cap and mask; slots past the context are not part of the softmax.
   const float inv_cap = 1.f / p.softcap;
-  float s[8];
-  float mx = -__builtin_inff();
-#pragma unroll
-  for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int t = 16 * nt + 4 * m + r;
-      const int dr = t - col;
-      const float rel = xs[col * 17 + min(max(dr, 0), 15)];
-      const float sc = st[nt][r] + ((dr >= 0 && dr < R) ? rel : 0.f);
-      const float capped = tanhf(sc * inv_cap) * p.softcap;
-      const int key = u * C - p.past + t;
-      const int distance = query - key;
-      bool allowed = distance >= 0 && distance < p.past;
-      if (p.future > 0) allowed = allowed || (distance < 0 && -distance < p.future);
-      allowed = allowed && key >= 0 && key < n;
-      const float v = t >= ctx ? -__builtin_inff() : allowed ? capped : p.invalid;
-      s[4 * nt + r] = v;
-      mx = fmaxf(mx, v);
-    }
-  // A query's slots live in lanes col, col + 16, col + 32, col + 48.
-  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-  float sum = 0.f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    s[i] = expf(s[i] - mx);  // natural exponent, as F.softmax; 0 past the context
-    sum += s[i];
-  }
-  sum += __shfl_xor(sum, 16, 64);
-  sum += __shfl_xor(sum, 32, 64);
+  float* xs = Xs + wave * 16 * 17;
+  for (int run = r0; run < r1; ++run) {
+    const int u = run * nblk + wave;
+    const int query = u * C + col;
+    const bool qok = col < C && query < p.tokens;
 
-  // O^T = V^T . P^T: step (nt, r) takes slot 16 nt + 4 m + r in k slot m,
-  // the same slot this lane's P^T register holds.
-  f32x4_t ot[KS / 4];
+    // S^T: context slot 16 nt + col against query column col.
+    f32x4_t st[2];
 #pragma unroll
-  for (int d = 0; d < KS / 4; ++d) ot[d] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int nt = 0; nt < 2; ++nt) {
+      st[nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt)
+      for (int d = 0; d < KS; ++d) st[nt] = mfma16(kv[nt][d], qv[d], st[nt]);
+    }
+    // Relative scores R^T[row][query]; lane holds rows 4 m + r of column col.
+    f32x4_t rt = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    {
+      const float* rr = Rs + col * RS + 4 * m;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int t = 16 * nt + 4 * m + r;
-      const bool in = t < ctx;
-      const float* vr = Vs + min(wave * C + t, rows - 1) * RS + col;
-#pragma unroll
-      for (int d = 0; d < KS / 4; ++d) {
-        const float x = vr[16 * d];
-        ot[d] = mfma16(in ? x : 0.f, s[4 * nt + r], ot[d]);
+      for (int d = 0; d < KS; d += 4) {
+        const float4 rv = *reinterpret_cast<const float4*>(rr + 4 * d);
+        rt = mfma16(rv.x, qv[d], rt);
+        rt = mfma16(rv.y, qv[d + 1], rt);
+        rt = mfma16(rv.z, qv[d + 2], rt);
+        rt = mfma16(rv.w, qv[d + 3], rt);
       }
     }
-  if (!qok) return;
-  const float inv = 1.f / sum;
-  float* op = p.out + (int64_t)b * p.o_batch_stride + (int64_t)query * p.o_token_stride +
-              (int64_t)h * p.o_head_stride + 4 * m;
+    // The next run's queries and keys go out now, into the registers just
+    // freed, and arrive while this run finishes.
+    const bool more = run + 1 < r1;
+    if (more) {
+      __builtin_amdgcn_sched_barrier(0);
+      load_qk(run + 1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // The reference's relative shift: slot t of query c adds relative row
+    // t - c when 0 <= t - c < R; rows move between lanes through LDS.
 #pragma unroll
-  for (int d = 0; d < KS / 4; ++d)
-    *reinterpret_cast<float4*>(op + 16 * d) =
-        make_float4(ot[d][0] * inv, ot[d][1] * inv, ot[d][2] * inv, ot[d][3] * inv);
+    for (int r = 0; r < 4; ++r) xs[col * 17 + 4 * m + r] = rt[r];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // Soft cap and mask; slots past the context are not part of the softmax.
+    float s[8];
+    float mx = -__builtin_inff();
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int t = 16 * nt + 4 * m + r;
+        const int dr = t - col;
+        const float rel = xs[col * 17 + min(max(dr, 0), 15)];
+        const float sc = st[nt][r] + ((dr >= 0 && dr < R) ? rel : 0.f);
+        const float capped = tanhf(sc * inv_cap) * p.softcap;
+        const int key = u * C - p.past + t;
+        const int distance = query - key;
+        bool allowed = distance >= 0 && distance < p.past;
+        if (p.future > 0) allowed = allowed || (distance < 0 && -distance < p.future);
+        allowed = allowed && key >= 0 && key < n;
+        const float v = t >= ctx ? -__builtin_inff() : allowed ? capped : p.invalid;
+        s[4 * nt + r] = v;
+        mx = fmaxf(mx, v);
+      }
+    // A query's slots live in lanes col, col + 16, col + 32, col + 48.
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      s[i] = expf(s[i] - mx);  // natural exponent, as F.softmax; 0 past the context
+      sum += s[i];
+    }
+    sum += __shfl_xor(sum, 16, 64);
+    sum += __shfl_xor(sum, 32, 64);
+
+    // This run's values into LDS once every wave is done with the last
+    // run's; then the next run's first values go out.
+    __syncthreads();
+    stage_rest(run);
+    __syncthreads();
+    if (more) load_v(run + 1, tid);
+
+    // O^T = V^T . P^T: step (nt, r) takes slot 16 nt + 4 m + r in k slot m,
+    // the same slot this lane's P^T register holds.
+    f32x4_t ot[KS / 4];
+#pragma unroll
+    for (int d = 0; d < KS / 4; ++d) ot[d] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int t = 16 * nt + 4 * m + r;
+        const bool in = t < ctx;
+        const float* vr = Vs + min(wave * C + t, rows - 1) * RS + col;
+#pragma unroll
+        for (int d = 0; d < KS / 4; ++d) {
+          const float x = vr[16 * d];
+          ot[d] = mfma16(in ? x : 0.f, s[4 * nt + r], ot[d]);
+        }
+      }
+    if (qok) {
+      const float inv = 1.f / sum;
+      float* op = p.out + (int64_t)b * p.o_batch_stride + (int64_t)query * p.o_token_stride +
+                  (int64_t)h * p.o_head_stride + 4 * m;
+#pragma unroll
+      for (int d = 0; d < KS / 4; ++d)
+        *reinterpret_cast<float4*>(op + 16 * d) =
+            make_float4(ot[d][0] * inv, ot[d][1] * inv, ot[d][2] * inv, ot[d][3] * inv);
+    }
+  }
 }
 
 // Blocks (waves) per workgroup of local_mfma_kernel; 0: the shape does not
@@ -246,6 +311,22 @@ int mfma_blocks(const asrattn_local_params& p) {
   for (int nblk = kMfmaMaxWaves; nblk > 0; --nblk)
     if (sizeof(float) * mfma_lds_floats(p, nblk) <= kMfmaLdsBudget) return nblk;
   return 0;
+}
+
+// Runs per workgroup of local_mfma_kernel: as few as let the whole grid be
+// resident at once (two waves per SIMD, the LDS per CU), so that every
+// workgroup's next run loads while its current one computes instead of a
+// second round of workgroups loading after the first has finished.
+int mfma_runs_per_workgroup(const asrattn_local_params& p, int nblk, int runs, size_t lds) {
+  int device = 0, cus = 0;
+  if (hipGetDevice(&device) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || cus <= 0)
+    cus = 256;
+  const int per_cu = std::max(1, std::min(8 / nblk, (int)(160 * 1024 / lds)));
+  const long long slots = (long long)cus * per_cu;
+  const long long total = (long long)runs * p.heads * p.batch;
+  const long long rpw = (total + slots - 1) / slots;
+  return (int)std::max(1LL, std::min(rpw, (long long)runs));
 }
 
 constexpr int kLocalThreads = 64;
@@ -351,12 +432,14 @@ hipError_t launch_local(const asrattn_local_params& p, hipStream_t stream) {
   const int blocks = (p.tokens + p.chunk - 1) / p.chunk;
   const int nblk = mfma_blocks(p);
   if (nblk > 0) {
-    const dim3 grid((unsigned)((blocks + nblk - 1) / nblk), (unsigned)p.heads, (unsigned)p.batch);
+    const int runs = (blocks + nblk - 1) / nblk;
     const size_t lds = sizeof(float) * mfma_lds_floats(p, nblk);
+    const int rpw = p.head_dim == 192 ? 1 : mfma_runs_per_workgroup(p, nblk, runs, lds);
+    const dim3 grid((unsigned)((runs + rpw - 1) / rpw), (unsigned)p.heads, (unsigned)p.batch);
     switch (p.head_dim) {
-      case 64: hipLaunchKernelGGL(local_mfma_kernel<16>, grid, dim3(64 * nblk), lds, stream, p, nblk); break;
-      case 128: hipLaunchKernelGGL(local_mfma_kernel<32>, grid, dim3(64 * nblk), lds, stream, p, nblk); break;
-      default: hipLaunchKernelGGL(local_mfma_kernel<48>, grid, dim3(64 * nblk), lds, stream, p, nblk); break;
+      case 64: hipLaunchKernelGGL(local_mfma_kernel<16>, grid, dim3(64 * nblk), lds, stream, p, nblk, rpw); break;
+      case 128: hipLaunchKernelGGL(local_mfma_kernel<32>, grid, dim3(64 * nblk), lds, stream, p, nblk, rpw); break;
+      default: hipLaunchKernelGGL(local_mfma_kernel<48>, grid, dim3(64 * nblk), lds, stream, p, nblk, rpw); break;
     }
     return hipGetLastError();
   }

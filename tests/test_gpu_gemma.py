@@ -76,6 +76,29 @@ def test_local_attention_matches_oracle(device, heads, head_dim, future):
     assert max_rel_err(out.cpu(), ref) < 1e-5
 
 
+@pytest.mark.parametrize("head_dim,frames", [(128, 500), (64, 620)])
+def test_local_attention_workgroups_walk_runs(device, head_dim, frames):
+    """Enough runs of four blocks that a workgroup takes two in a row,
+    loading the second while it computes the first (8 sequences x 8 heads of
+    500 tokens: 11 runs per (sequence, head), 704 in all for 512 resident
+    workgroups; the last workgroup of each pair of heads gets one), with
+    ragged lengths."""
+    from asrback_amd import attention
+
+    say("local attention runs", head_dim, frames)
+    chunk, past, heads, batch = 12, 12, 8, 8
+    lengths = torch.tensor([frames, 431, 17, frames - 1, 250, 1, frames, 333], dtype=torch.int32)
+    q = randn(batch, frames, heads, head_dim, seed=11, scale=0.3)
+    k = randn(batch, frames, heads, head_dim, seed=12)
+    v = randn(batch, frames, heads, head_dim, seed=13)
+    rel = randn(13, heads, head_dim, seed=14, scale=0.3)
+    mask = og.blocked_mask(lengths, frames, chunk, past, 0)
+    ref = og.local_attention(q, k, v, rel, mask, chunk, past, 0, 50.0, -1e9)
+    out = attention.local_attention(q.to(device), k.to(device), v.to(device), rel.to(device), lengths.to(device),
+                                    chunk=chunk, past=past, future=0, softcap=50.0, invalid=-1e9)
+    assert max_rel_err(out.cpu(), ref) < 1e-5
+
+
 def test_audio_attention_module_matches_oracle(device):
     """``AudioAttention.forward(x, positions, mask)`` with its clipped
     projections, per-dimension query scale and relative-key projection
