@@ -19,12 +19,15 @@ int decode_keys_per_wave(int dtype, int head_dim) {
 }
 
 int decode_waves(const asrattn_decode_params& p, int splits, int page_size) {
-  // Enough waves in flight to keep HBM busy: about 16 per CU over the grid,
-  // but no more than one load batch of the split's keys needs (Whisper's
-  // 256-key self-attention bucket: 8 waves, 4% faster than 16).
+  // About 2048 waves over the grid (two per SIMD): on one MI355X, Qwen3's
+  // 512 workgroups ran 6% faster on 4 waves than on 8, Gemma 4's 256 5%
+  // faster on 8 than on 16, Whisper's 192 the same on 8 and 16.  No more
+  // waves than one load batch of the split's keys needs (Whisper's 256-key
+  // self-attention bucket: 8 waves, 4% faster than 16).
   const long long groups = (long long)p.batch * p.heads_kv * splits;
   const int keys_per_split = (p.max_len_k + splits - 1) / splits;
-  int waves = groups >= 1024 ? 4 : groups >= 384 ? 8 : 16;
+  int waves = 16;
+  while (waves > 4 && groups * waves > 2048) waves /= 2;
   // A wave loads 64 / LPK rows per instruction (8 for bf16 x 64, 4 for 128),
   // and a batch takes 4 of them (2 with four or more query heads per kv
   // head, or head_dim 256 and up: DecodeShape::kUnroll).
