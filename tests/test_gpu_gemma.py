@@ -76,26 +76,27 @@ def test_local_attention_matches_oracle(device, heads, head_dim, future):
     assert max_rel_err(out.cpu(), ref) < 1e-5
 
 
-@pytest.mark.parametrize("head_dim,frames", [(128, 500), (64, 620)])
-def test_local_attention_workgroups_walk_runs(device, head_dim, frames):
+@pytest.mark.parametrize("head_dim,frames,future", [(128, 500, 0), (64, 620, 0), (64, 620, 3)])
+def test_local_attention_workgroups_walk_runs(device, head_dim, frames, future):
     """Enough runs of four blocks that a workgroup takes two in a row,
     loading the second while it computes the first (8 sequences x 8 heads of
     500 tokens: 11 runs per (sequence, head), 704 in all for 512 resident
     workgroups; the last workgroup of each pair of heads gets one), with
-    ragged lengths."""
+    ragged lengths; also with three keys past each block (14 relative
+    rows)."""
     from asrback_amd import attention
 
-    say("local attention runs", head_dim, frames)
+    say("local attention runs", head_dim, frames, future)
     chunk, past, heads, batch = 12, 12, 8, 8
     lengths = torch.tensor([frames, 431, 17, frames - 1, 250, 1, frames, 333], dtype=torch.int32)
     q = randn(batch, frames, heads, head_dim, seed=11, scale=0.3)
     k = randn(batch, frames, heads, head_dim, seed=12)
     v = randn(batch, frames, heads, head_dim, seed=13)
-    rel = randn(13, heads, head_dim, seed=14, scale=0.3)
-    mask = og.blocked_mask(lengths, frames, chunk, past, 0)
-    ref = og.local_attention(q, k, v, rel, mask, chunk, past, 0, 50.0, -1e9)
+    rel = randn((chunk + past + future) // 2 + 1, heads, head_dim, seed=14, scale=0.3)
+    mask = og.blocked_mask(lengths, frames, chunk, past, future)
+    ref = og.local_attention(q, k, v, rel, mask, chunk, past, future, 50.0, -1e9)
     out = attention.local_attention(q.to(device), k.to(device), v.to(device), rel.to(device), lengths.to(device),
-                                    chunk=chunk, past=past, future=0, softcap=50.0, invalid=-1e9)
+                                    chunk=chunk, past=past, future=future, softcap=50.0, invalid=-1e9)
     assert max_rel_err(out.cpu(), ref) < 1e-5
 
 
