@@ -275,6 +275,50 @@ def test_decode_zero_keys_gives_zeros(ops, device):
     assert torch.count_nonzero(out[1]) > 0
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("hd,heads_q,heads_kv", [(128, 16, 8), (64, 12, 12)])
+@pytest.mark.parametrize("splits", [1, 3])
+def test_decode_ignores_cache_slots_past_each_row(ops, device, dtype, hd, heads_q, heads_kv, splits):
+    """Cache slots at and past each row's length hold NaN (a slab row used
+    before, or never written).  With one split the first load batch reads
+    the whole row before its length is known; the outputs still equal the
+    oracle's over each row's own keys, for plain decode (seqused_k) and the
+    append variant (the step's key at the row's position), and a row of
+    length 0 gives zeros."""
+    say("decode past rows", dtype, hd, heads_q, heads_kv, splits)
+    batch, length = 6, 320
+    n = torch.tensor([0, 1, 37, 64, 200, 319])
+    q = randn(batch, heads_q, hd, seed=81, dtype=dtype)
+    keys = randn(batch, length, heads_kv, hd, seed=82, dtype=dtype)
+    values = randn(batch, length, heads_kv, hd, seed=83, dtype=dtype)
+    past = torch.arange(length)[None, :] >= n[:, None]
+    keys_nan, values_nan = keys.clone(), values.clone()
+    keys_nan[past] = float("nan")
+    values_nan[past] = float("nan")
+    mask = torch.arange(length)[None, :] < n[:, None]
+    ref = oa.qwen_step_attention(q.float(), keys.float(), values.float(), mask[:, None, None, :])
+    used = n.to(torch.int32).to(device)
+    out = ops.decode(q.to(device), keys_nan.to(device), values_nan.to(device), seqused_k=used,
+                     num_splits=splits).float().cpu()
+    assert torch.count_nonzero(out[0]) == 0
+    assert max_rel_err(out[1:], ref[1:]) < TOL[dtype]
+
+    # Append: row b's step key goes to slot n_b and attends keys 0..n_b.
+    positions = n.clone()
+    k_new = randn(batch, heads_kv, hd, seed=84, dtype=dtype)
+    v_new = randn(batch, heads_kv, hd, seed=85, dtype=dtype)
+    rows = torch.arange(batch)
+    keys_ref, values_ref = keys.clone(), values.clone()
+    keys_ref[rows, positions] = k_new
+    values_ref[rows, positions] = v_new
+    ref = oa.qwen_step_attention(q.float(), keys_ref.float(), values_ref.float(), oa.qwen_step_mask(positions, length))
+    kd, vd = keys_nan.to(device), values_nan.to(device)
+    out = ops.decode_append(q.to(device), k_new.to(device), v_new.to(device), kd, vd, positions.to(device),
+                            num_splits=splits)
+    assert max_rel_err(out.float().cpu(), ref) < TOL[dtype]
+    assert torch.equal(kd.cpu()[rows, positions], k_new) and torch.equal(vd.cpu()[rows, positions], v_new)
+
+
 def test_encoder_zero_keys_gives_zeros(ops, device):
     q = randn(2, 40, 2, 128, seed=34, dtype=torch.bfloat16).to(device)
     used = torch.tensor([0, 17], dtype=torch.int32, device=device)
