@@ -37,7 +37,7 @@ extern "C" {
 enum asrattn_status {
   ASRATTN_OK = 0,
   ASRATTN_ERR_INVALID = 1,      /* bad argument (shape, stride, pointer) */
-  ASRATTN_ERR_UNSUPPORTED = 2,  /* valid request this build has no kernel for */
+  ASRATTN_ERR_UNSUPPORTED = 2,  /* valid request the library has no kernel for */
   ASRATTN_ERR_HIP = 3,          /* the HIP runtime reported an error */
   ASRATTN_ERR_WORKSPACE = 4     /* workspace missing or too small */
 };
