@@ -152,9 +152,16 @@ __device__ __forceinline__ int ranked_sequence(const asrattn_fwd_params& p, int 
   return __ffsll(hit) - 1;  // ranks are a permutation: exactly one lane
 }
 
+// Ranking costs every workgroup a round trip for all sequences' key
+// counts before its own loads; it pays only when items differ by more than
+// a couple of tiles (SenseVoice, up to 504 keys: 22.8 against 24.4 us
+// unranked; Qwen3's audio windows of at most 104 keys: 11.9 against 10.5).
+constexpr int kRankMinKeys = 128;
+
 // Launch id -> (sequence, query head, query tile).  Dispatch hands ids out
 // in order as workgroup slots free up, round-robin over the 8 XCDs.  With
-// per-sequence key counts (ragged batches of at most 64 sequences) the
+// per-sequence key counts (ragged batches of at most 64 sequences, some
+// longer than kRankMinKeys) the
 // (sequence, kv head) units are taken in decreasing key count -- the
 // longest work starts first and short units fill in behind it -- and unit U
 // goes to XCD U % 8 with all its items consecutive there (every query head
@@ -166,7 +173,7 @@ __device__ __forceinline__ int ranked_sequence(const asrattn_fwd_params& p, int 
 __device__ __forceinline__ void work_item(const asrattn_fwd_params& p, int q_tiles, int total, int id, int& b,
                                           int& hq, int& qt) {
   const bool ragged = p.seqused_k != nullptr || p.cu_seqlens_k != nullptr;
-  if (ragged && p.batch <= 64 && (p.batch * p.heads_kv) % 8 == 0) {
+  if (ragged && p.max_len_k > kRankMinKeys && p.batch <= 64 && (p.batch * p.heads_kv) % 8 == 0) {
     const int group = p.heads_q / p.heads_kv;
     const int per_unit = group * q_tiles;
     const int per = total / 8, half = per / 2;
