@@ -100,6 +100,15 @@ __global__ __launch_bounds__(64 * kMfmaMaxWaves, 2) void local_mfma_kernel(const
   // columns past the block and slots past the context read nothing (an
   // offset past every range; their results are never stored or are dropped
   // from the softmax below).
+  // Context slot of row 4 mm + r of score tile nt, or -1.  With at most 24
+  // slots the second tile's (at most 8) sit in its rows 4 mm + {0, 1}, so
+  // the value product skips that tile's steps r = 2, 3.
+  const bool packed = ctx <= 24;
+  auto slot_of = [&](int nt, int mm, int r) -> int {
+    if (nt == 0) return 4 * mm + r;
+    if (packed) return r < 2 ? 16 + 2 * mm + r : -1;
+    return 16 + 4 * mm + r;
+  };
   float qv[KS], kv[2][KS];
   auto load_qk = [&](int run) {
     constexpr uint32_t kNowhere = 0x80000000u;  // past any range (ranges stay below 2^31)
@@ -108,7 +117,8 @@ __global__ __launch_bounds__(64 * kMfmaMaxWaves, 2) void local_mfma_kernel(const
     const uint32_t qo = col < C ? (uint32_t)(u * C + col) * qts + dim0 : kNowhere;
     const int key = u * C - p.past + col;
     const uint32_t ko0 = col < ctx ? (uint32_t)key * kts + dim0 : kNowhere;
-    const uint32_t ko1 = 16 + col < ctx ? (uint32_t)(key + 16) * kts + dim0 : kNowhere;
+    const int t1 = slot_of(1, col >> 2, col & 3);  // the slot of tile 1's row col
+    const uint32_t ko1 = t1 >= 0 && t1 < ctx ? (uint32_t)(key - col + t1) * kts + dim0 : kNowhere;
 #pragma unroll
     for (int d = 0; d < KS; d += 4) {
       const float4 t = __builtin_bit_cast(float4, buffer_load16(qrs, qo + d * 16));
@@ -224,7 +234,7 @@ __global__ __launch_bounds__(64 * kMfmaMaxWaves, 2) void local_mfma_kernel(const
     for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int t = 16 * nt + 4 * m + r;
+        const int t = slot_of(nt, m, r);
         const int dr = t - col;
         const float rel = xs[col * 17 + min(max(dr, 0), 15)];
         const float sc = st[nt][r] + ((dr >= 0 && dr < R) ? rel : 0.f);
@@ -234,7 +244,7 @@ __global__ __launch_bounds__(64 * kMfmaMaxWaves, 2) void local_mfma_kernel(const
         bool allowed = distance >= 0 && distance < p.past;
         if (p.future > 0) allowed = allowed || (distance < 0 && -distance < p.future);
         allowed = allowed && key >= 0 && key < n;
-        const float v = t >= ctx ? -__builtin_inff() : allowed ? capped : p.invalid;
+        const float v = t < 0 || t >= ctx ? -__builtin_inff() : allowed ? capped : p.invalid;
         s[4 * nt + r] = v;
         mx = fmaxf(mx, v);
       }
@@ -257,8 +267,8 @@ __global__ __launch_bounds__(64 * kMfmaMaxWaves, 2) void local_mfma_kernel(const
     __syncthreads();
     if (more) load_v(run + 1, tid);
 
-    // O^T = V^T . P^T: step (nt, r) takes slot 16 nt + 4 m + r in k slot m,
-    // the same slot this lane's P^T register holds.
+    // O^T = V^T . P^T: step (nt, r) takes slot slot_of(nt, m, r) in k slot
+    // m, the same slot this lane's P^T register holds.
     f32x4_t ot[KS / 4];
 #pragma unroll
     for (int d = 0; d < KS / 4; ++d) ot[d] = f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -266,9 +276,10 @@ __global__ __launch_bounds__(64 * kMfmaMaxWaves, 2) void local_mfma_kernel(const
     for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int t = 16 * nt + 4 * m + r;
-        const bool in = t < ctx;
-        const float* vr = Vs + min(wave * C + t, rows - 1) * RS + col;
+        if (nt == 1 && packed && r >= 2) continue;  // uniform: rows without a slot
+        const int t = slot_of(nt, m, r);
+        const bool in = t >= 0 && t < ctx;
+        const float* vr = Vs + min(wave * C + max(t, 0), rows - 1) * RS + col;
 #pragma unroll
         for (int d = 0; d < KS / 4; ++d) {
           const float x = vr[16 * d];
