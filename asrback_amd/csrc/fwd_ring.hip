@@ -69,6 +69,7 @@ __device__ __forceinline__ f32x16_t mfma32(const bf16x8_t& a, const bf16x8_t& b,
 
 // LDS reads by byte address, so that constant parts of an address fold
 // into the instruction's offset field.
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ bf16x8_t lds_read16(uint32_t addr) { return *(lds_bf16x8_ptr)(size_t)addr; }
 
 // Transpose load of 4 bf16: within each 16-lane group, lane j receives
@@ -621,7 +622,9 @@ __global__ __launch_bounds__(64 * RB * KS * DS, OCC) void fwd_ring_kernel(const 
     const uint4 val = *reinterpret_cast<const uint4*>(stage + r * ORS + col);
     if (orow < sv.len_q) {
       bf16_raw* op = static_cast<bf16_raw*>(p.out) + sv.o_off + (int64_t)orow * p.o_token_stride + col;
-      *reinterpret_cast<uint4*>(op) = val;
+      // Nontemporal: the output is not read again in this launch (Qwen3's
+      // prompt pass 20.2 -> 19.3 us, SenseVoice -1%).
+      __builtin_nontemporal_store(__builtin_bit_cast(u32x4_t, val), reinterpret_cast<u32x4_t*>(op));
     }
   }
 }
