@@ -19,7 +19,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must be imported before the library; see above)
 
 LIBRARY = Path(__file__).resolve().with_name("libasrattn.so")
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 # enum asrattn_status / asrattn_dtype / asrattn_causal
 OK = 0
@@ -33,6 +33,7 @@ CAUSAL_NONE = 0
 CAUSAL_TOP_LEFT = 1
 CAUSAL_BOTTOM_RIGHT = 2
 FWD_FORCE_VALU = 1
+FWD_ZERO_PADDED_ROWS = 2
 
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int32

@@ -25,8 +25,8 @@ itself), :func:`flash_fsmn` (SenseVoice attention plus its FSMN memory),
 write) and :func:`greedy_choice` (argmax and its log-probability).
 
 The reference's masks are all prefix masks: each query row sees keys
-``0 .. n-1`` (optionally causal on top).  General boolean masks are not
-supported.
+``0 .. n-1`` (optionally causal on top).  A boolean mask with a hole is
+refused (:meth:`KeyPrefix.from_mask`).
 """
 
 from __future__ import annotations
@@ -68,10 +68,25 @@ class KeyPrefix:
     @classmethod
     def from_mask(cls, mask: Tensor) -> KeyPrefix:
         """The prefix described by a boolean ``(batch, 1, 1, length)`` or
-        ``(batch, length)`` mask that is True for keys ``0 .. n_b - 1``."""
+        ``(batch, length)`` mask that is True for keys ``0 .. n_b - 1``.
+
+        A mask with a hole (a False before a True in some row) describes an
+        attention the kernels do not compute: it raises ``ValueError``.  The
+        check reads the comparison back from the device, so a tensor mask is
+        refused during graph capture (pass a :class:`KeyPrefix` there, as
+        every module of this package does)."""
         if mask.dtype != torch.bool:
             raise TypeError(f"only boolean prefix masks are supported, got {mask.dtype}")
-        lengths = mask.reshape(mask.shape[0], mask.shape[-1]).sum(dim=-1, dtype=torch.int32)
+        if mask.dim() < 2 or mask.numel() != mask.shape[0] * mask.shape[-1]:
+            raise ValueError(f"expected a (batch, length) or (batch, 1, 1, length) mask, got {tuple(mask.shape)}")
+        if mask.is_cuda and torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("a boolean mask cannot be checked during graph capture; pass a KeyPrefix")
+        rows = mask.reshape(mask.shape[0], mask.shape[-1])
+        lengths = rows.sum(dim=-1, dtype=torch.int32)
+        prefix = torch.arange(rows.shape[-1], device=rows.device)[None, :] < lengths[:, None]
+        if not torch.equal(rows, prefix):
+            raise ValueError("the attention kernels take prefix masks only (row b sees keys 0 .. n_b - 1); "
+                             "this mask has a False before a True")
         return cls(lengths=lengths)
 
 
@@ -188,6 +203,7 @@ def _fwd_params(
     scale: float | None,
     force_valu: bool,
     window: int = 0,
+    flags: int = 0,
 ) -> tuple[_lib.FwdParams, Tensor, torch.device, tuple]:
     """``asrattn_fwd_params`` for :func:`flash`; returns them with ``out``,
     the device and the tensors the parameters point into (kept alive until
@@ -212,8 +228,9 @@ def _fwd_params(
     q, k, v = (_aligned(t, strided) for t in (q, k, v))
     if out is None:
         out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
-    elif out.shape != q.shape or out.dtype != q.dtype:
-        raise ValueError("out must match q's shape and dtype")
+    elif out.shape != q.shape or out.dtype != q.dtype or out.stride(-1) != 1:
+        # The kernels write each head's head_dim elements contiguously.
+        raise ValueError("out must match q's shape and dtype, with a unit last stride")
     device = _check_device(q, k, v, out, cu_seqlens_q, cu_seqlens_k, seqused_k)
     cu_seqlens_q = _int32(cu_seqlens_q, "cu_seqlens_q")
     cu_seqlens_k = _int32(cu_seqlens_k, "cu_seqlens_k")
@@ -257,7 +274,7 @@ def _fwd_params(
     params.causal = causal
     params.dtype = dtype
     params.scale = 1.0 / math.sqrt(head_dim) if scale is None else scale
-    params.flags = _lib.FWD_FORCE_VALU if force_valu else 0
+    params.flags = flags | (_lib.FWD_FORCE_VALU if force_valu else 0)
     params.window = window or 0
     return params, out, device, (q, k, v, cu_seqlens_q, cu_seqlens_k, seqused_k)
 
@@ -277,19 +294,23 @@ def flash(
     scale: float | None = None,
     force_valu: bool = False,
     window: int | None = None,
+    zero_padded_rows: bool = False,
 ) -> Tensor:
     """Multi-row attention (``asrattn_fwd``).  ``window`` (causal only):
     each query also skips keys more than ``window - 1`` before its last
-    visible one (sliding-window attention).
+    visible one (sliding-window attention).  ``zero_padded_rows`` (padded,
+    non-causal, with ``seqused_k``): query rows at or past a sequence's key
+    count are not computed and get zeros; the other rows are unchanged.
 
     Padded layout: ``q`` ``(batch, len_q, heads_q, head_dim)``, ``k``/``v``
     ``(batch, len_k, heads_kv, head_dim)``; packed layout (``cu_seqlens_*``
     given): ``(tokens, heads, head_dim)``.  Returns ``out`` in ``q``'s layout
     (a new contiguous tensor unless ``out`` is given).
     """
+    flags = _lib.FWD_ZERO_PADDED_ROWS if zero_padded_rows else 0
     params, out, device, keep = _fwd_params(
         q, k, v, out, causal, cu_seqlens_q, cu_seqlens_k, max_len_q, max_len_k, seqused_k, scale, force_valu,
-        window or 0,
+        window or 0, flags,
     )
     lib = _lib.load()
     _lib.check(lib.asrattn_fwd(ctypes.byref(params), _stream(device)), "asrattn_fwd")
@@ -309,6 +330,7 @@ def flash_fsmn(
     memory: Tensor | None = None,
     scale: float | None = None,
     force_valu: bool = False,
+    zero_padded_rows: bool = False,
 ) -> tuple[Tensor, Tensor]:
     """SAN-M self-attention and its FSMN memory in one call
     (``asrattn_fwd_fsmn``; ``sensevoice.py:97-135``).
@@ -318,7 +340,9 @@ def flash_fsmn(
     frame is real), ``weight`` the depthwise Conv1d weight ``(C, 1, K)`` or
     ``(C, K)`` with ``C = heads * head_dim``.  Returns ``(out, memory)``,
     ``memory`` ``(batch, frames, C)`` = the reference's FSMN memory plus
-    ``bias`` (if given) on every row.
+    ``bias`` (if given) on every row.  ``zero_padded_rows`` (with
+    ``seqused_k``): attention rows of frames at or past a sequence's count
+    are zeros instead of computed; the memory is unaffected.
     """
     if q.shape != k.shape or q.shape != v.shape:
         raise ValueError("the FSMN path needs q, k and v of one shape (batch, frames, heads, head_dim)")
@@ -338,7 +362,8 @@ def flash_fsmn(
     elif memory.shape != (batch, frames, channels) or memory.dtype != q.dtype or memory.stride(-1) != 1:
         raise ValueError("memory must be a (batch, frames, channels) tensor of q's dtype with unit channel stride")
     params, out, device, keep = _fwd_params(
-        q, k, v, out, _lib.CAUSAL_NONE, None, None, None, None, seqused_k, scale, force_valu
+        q, k, v, out, _lib.CAUSAL_NONE, None, None, None, None, seqused_k, scale, force_valu, 0,
+        _lib.FWD_ZERO_PADDED_ROWS if zero_padded_rows else 0,
     )
     _check_device(q, weight, bias, memory)
     f = _lib.FsmnParams()

@@ -143,6 +143,10 @@ int check_fwd(const asrattn_fwd_params* params, bool* empty) {
     return fail(ASRATTN_ERR_INVALID, "cu_seqlens_q and cu_seqlens_k must both be set or both be NULL");
   if (p.window < 0 || (p.window > 0 && p.causal == ASRATTN_CAUSAL_NONE))
     return fail(ASRATTN_ERR_INVALID, "window must be >= 0, and > 0 only with causal attention (got %d)", p.window);
+  if ((p.flags & ASRATTN_FWD_ZERO_PADDED_ROWS) != 0 &&
+      (p.cu_seqlens_q != nullptr || p.causal != ASRATTN_CAUSAL_NONE || p.seqused_k == nullptr))
+    return fail(ASRATTN_ERR_INVALID,
+                "ASRATTN_FWD_ZERO_PADDED_ROWS needs the padded, non-causal layout with seqused_k");
   *empty = p.batch == 0 || p.max_len_q == 0;
   if (*empty) return ASRATTN_OK;
   if (p.q == nullptr || p.k == nullptr || p.v == nullptr || p.out == nullptr)

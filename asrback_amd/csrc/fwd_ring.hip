@@ -52,58 +52,12 @@
 #include "common.hpp"
 #include "fwd_common.hpp"
 #include "kernels.hpp"
+#include "ring_common.hpp"
 
 namespace asrattn {
 namespace {
 
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef short short4_t __attribute__((ext_vector_type(4)));
-typedef short short8_t __attribute__((ext_vector_type(8)));
-typedef float f32x16_t __attribute__((ext_vector_type(16)));
-typedef __attribute__((address_space(3))) short4_t* lds_short4_ptr;
-typedef __attribute__((address_space(3))) const bf16x8_t* lds_bf16x8_ptr;
-
-__device__ __forceinline__ f32x16_t mfma32(const bf16x8_t& a, const bf16x8_t& b, const f32x16_t& c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-}
-
-// LDS reads by byte address, so that constant parts of an address fold
-// into the instruction's offset field.
-typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ bf16x8_t lds_read16(uint32_t addr) { return *(lds_bf16x8_ptr)(size_t)addr; }
-
-// Transpose load of 4 bf16: within each 16-lane group, lane j receives
-// element (j % 4) of the 8-byte chunks addressed by lanes 4k + j / 4,
-// k = 0..3.
-__device__ __forceinline__ short4_t ds_read_tr(uint32_t addr) {
-  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_ptr)(size_t)addr);
-}
-
-// One DMA instruction: lane i copies the 16 bytes at buffer offset `voff`
-// into LDS bytes [lds_base + 16 i, +16).  Issued as inline assembly so that
-// the compiler's wait-count pass, which cannot tell ring stages apart, does
-// not drain every DMA before each LDS read; the kernel waits for them itself
-// (wait_dma).  M0 is saved and restored around the instruction.
-__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, uint32_t lds_base, uint32_t voff) {
-  uint32_t saved;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %1\n\t"
-      "s_nop 0\n\t"
-      "buffer_load_dwordx4 %2, %3, 0 offen lds\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(saved)
-      : "s"(lds_base), "v"(voff), "s"(rsrc)
-      : "memory");
-}
-
-// s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt in bits 3:0 and 15:14; expcnt
-// and lgkmcnt left at their maxima).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
-}
+using namespace ring;
 
 // Waits until at most `ahead` tiles' DMAs (PER instructions each) of this
 // wave are outstanding.
@@ -117,40 +71,6 @@ __device__ __forceinline__ void wait_dma(int ahead) {
   } else {
     wait_vmcnt<0>();
   }
-}
-
-// Id -> work item such that the ids one XCD receives (round-robin dispatch
-// over 8 XCDs) map to a contiguous range of items.
-__device__ __forceinline__ int xcd_remap(int id, int total) {
-  const int per = total / 8;
-  const int rem = total % 8;
-  const int x = id % 8;
-  const int k = id / 8;
-  return x * per + min(x, rem) + k;
-}
-
-// Workgroup of RB row blocks x KS key splits (one wave each); a ring stage
-// holds KS consecutive BN-key sub-tiles, split ks taking the ks-th.
-// Visible keys of sequence b before any causal limit.
-__device__ __forceinline__ int sequence_keys(const asrattn_fwd_params& p, int b) {
-  int n = p.cu_seqlens_k != nullptr ? p.cu_seqlens_k[b + 1] - p.cu_seqlens_k[b] : p.max_len_k;
-  n = min(max(n, 0), p.max_len_k);
-  if (p.seqused_k != nullptr) n = min(n, max(p.seqused_k[b], 0));
-  return n;
-}
-
-// The sequence of rank r in decreasing key count (ties in index order), for
-// batches of at most 64: lane b ranks sequence b against all others.
-__device__ __forceinline__ int ranked_sequence(const asrattn_fwd_params& p, int r) {
-  const int lane = threadIdx.x & 63;
-  const int n = lane < p.batch ? sequence_keys(p, lane) : -1;
-  int rank = 0;
-  for (int j = 0; j < p.batch; ++j) {
-    const int nj = __builtin_amdgcn_readlane(n, j);
-    rank += (nj > n || (nj == n && j < lane)) ? 1 : 0;
-  }
-  const unsigned long long hit = __ballot(lane < p.batch && rank == r);
-  return __ffsll(hit) - 1;  // ranks are a permutation: exactly one lane
 }
 
 // Ranking costs every workgroup a round trip for all sequences' key
@@ -235,25 +155,6 @@ struct RingShape {
   static_assert(DS == 1 || (KS == 1 && kKSteps % 8 == 0), "dimension splits: one key split, whole 256-byte groups");
 };
 
-// Physical chunk of logical chunk c in row r of a K tile, and its inverse;
-// rows of more than 16 chunks (head_dim 256, 512) rotate within each group
-// of 16 chunks.
-template <int HD>
-__device__ __forceinline__ int k_phys(int r, int c) {
-  if constexpr (HD == 64) return (c + (r >> 1)) & 7;
-  return (c & ~15) | ((c + r) & 15);
-}
-template <int HD>
-__device__ __forceinline__ int k_logical(int r, int pc) {
-  if constexpr (HD == 64) return (pc - (r >> 1)) & 7;
-  return (pc & ~15) | ((pc - r) & 15);
-}
-// V tiles: an XOR, its own inverse.
-template <int HD>
-__device__ __forceinline__ int v_phys(int r, int c) {
-  return HD == 64 ? (c ^ (4 * ((r >> 1) & 1))) : (c ^ (4 * (r & 3)));
-}
-
 template <int HD, int RB, int KS, int BN, int ST, int OCC, int FS, bool WIN, int DS>
 __global__ __launch_bounds__(64 * RB * KS * DS, OCC) void fwd_ring_kernel(const FwdArgs a, int q_tiles, int total) {
   using S = RingShape<HD, RB, KS, BN, ST, DS>;
@@ -290,6 +191,18 @@ __global__ __launch_bounds__(64 * RB * KS * DS, OCC) void fwd_ring_kernel(const 
   const SeqView sv = seq_view(p, b, hq, hkv);
   const int row0 = qt * BM;
   if (row0 >= sv.len_q) return;  // uniform over the workgroup
+  // Rows computed: [0, len_c).  With zero-padded rows a padded sequence's
+  // rows at or past its key count are not computed; they get zeros.
+  const int len_c = (p.flags & ASRATTN_FWD_ZERO_PADDED_ROWS) != 0 ? min(sv.len_q, sv.n_k) : sv.len_q;
+  if (row0 >= len_c) {
+    constexpr int kCPRz = HD / 8;
+    for (int ch = (int)threadIdx.x; ch < (min(row0 + BM, sv.len_q) - row0) * kCPRz; ch += S::kThreads) {
+      bf16_raw* op = static_cast<bf16_raw*>(p.out) + sv.o_off + (int64_t)(row0 + ch / kCPRz) * p.o_token_stride +
+                     (ch % kCPRz) * 8;
+      __builtin_nontemporal_store((u32x4_t){0u, 0u, 0u, 0u}, reinterpret_cast<u32x4_t*>(op));
+    }
+    return;  // uniform over the workgroup
+  }
 
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: DMA destinations live in SGPRs
@@ -300,19 +213,19 @@ __global__ __launch_bounds__(64 * RB * KS * DS, OCC) void fwd_ring_kernel(const 
   const int half = lane >> 5;
   const int wrow0 = row0 + 32 * rb;
   const int row = wrow0 + r32;
-  const bool row_ok = row < sv.len_q;
+  const bool row_ok = row < len_c;
   // Keys the workgroup (its last row) and this wave (its last row) see; with
   // a sliding window they start at the workgroup's first row's first key,
   // kofs, and the tiles count keys from there.
-  const int last = min(row0 + BM, sv.len_q) - 1;
-  const int wlast = min(wrow0 + 32, sv.len_q) - 1;
+  const int last = min(row0 + BM, len_c) - 1;
+  const int wlast = min(wrow0 + 32, len_c) - 1;
   const int kend = visible_keys(p, sv, last);
   const int kofs = WIN ? min(first_key(p, sv, row0), kend) : 0;
   const int n_tiles = (kend - kofs + SPAN - 1) / SPAN;
   const int row_lim = visible_keys(p, sv, row) - kofs;  // this row: keys [row_lo, row_lim) after kofs
   const int row_lo = WIN ? first_key(p, sv, row) - kofs : 0;
-  const int wkend = wrow0 < sv.len_q ? visible_keys(p, sv, wlast) - kofs : 0;
-  const int wkbeg = WIN && wrow0 < sv.len_q ? first_key(p, sv, wrow0) - kofs : 0;
+  const int wkend = wrow0 < len_c ? visible_keys(p, sv, wlast) - kofs : 0;
+  const int wkbeg = WIN && wrow0 < len_c ? first_key(p, sv, wrow0) - kofs : 0;
 
   // Low 32 bits of the flat address of an LDS variable are its LDS offset.
   const uint32_t lds_base = (uint32_t)(uintptr_t)lds;
@@ -407,8 +320,8 @@ __global__ __launch_bounds__(64 * RB * KS * DS, OCC) void fwd_ring_kernel(const 
   // of the wave sees fewer than all of its keys -- the wave's first row sees
   // the fewest -- or, with a window, some row's window starts inside it --
   // the wave's last row's starts latest).
-  const int wmin = wrow0 < sv.len_q ? visible_keys(p, sv, wrow0) - kofs : 0;
-  const int wlo = WIN && wrow0 < sv.len_q ? first_key(p, sv, wlast) - kofs : 0;
+  const int wmin = wrow0 < len_c ? visible_keys(p, sv, wrow0) - kofs : 0;
+  const int wlo = WIN && wrow0 < len_c ? first_key(p, sv, wlast) - kofs : 0;
   auto masked = [&](int kt) { return kt + BN > wmin || (WIN && kt < wlo); };
 
   // S^T of tile j (stage stage_idx) into s.
@@ -596,7 +509,7 @@ __global__ __launch_bounds__(64 * RB * KS * DS, OCC) void fwd_ring_kernel(const 
 
   // The half waves hold disjoint keys of the same rows.
   const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
-  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  const float inv = l_tot > 0.f && row_ok ? 1.f / l_tot : 0.f;  // rows past len_c get zeros
   // Accumulator r of block db is column 32 db + 8 (r / 4) + 4 half + r % 4
   // of row r32: write the normalized rows to LDS ...
 #pragma unroll

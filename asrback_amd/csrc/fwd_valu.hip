@@ -119,8 +119,10 @@ __global__ __launch_bounds__(kLanes) void fwd_valu_kernel(const FwdArgs a) {
 
   if (row_ok) {
     T* op = static_cast<T*>(p.out) + sv.o_off + (int64_t)row * p.o_token_stride + sub * DPL;
+    // Zero-padded rows: a padded sequence's rows at or past its key count.
+    const bool zero = (p.flags & ASRATTN_FWD_ZERO_PADDED_ROWS) != 0 && row >= sv.n_k;
 #pragma unroll
-    for (int d = 0; d < DPL; ++d) Elem<T>::store1(op + d, l > 0.f ? o[d] / l : 0.f);
+    for (int d = 0; d < DPL; ++d) Elem<T>::store1(op + d, l > 0.f && !zero ? o[d] / l : 0.f);
   }
 }
 

@@ -34,8 +34,9 @@ from .attention import KeyPrefix, decode, decode_append, decode_supported, flash
 
 
 class RMSNorm(nn.Module):
-    """Gemma 4's RMS norm, computed in float32; ``scale=False`` has no weight
-    (``gemma4.py:166-180``)."""
+    """Root-mean-square normalization as Gemma 4 applies it
+    (``gemma4.py:166-180``): the statistics in float32, then an optional
+    learned scale (none when ``scale=False``)."""
 
     def __init__(self, width: int, eps: float, scale: bool = True) -> None:
         super().__init__()
@@ -52,8 +53,8 @@ class RMSNorm(nn.Module):
 
 
 class ClippedLinear(nn.Module):
-    """A linear layer with its input and output clamped to the checkpoint's
-    ranges (``gemma4.py:183-197``)."""
+    """``nn.Linear`` between two clamps whose bounds come with the checkpoint
+    (``gemma4.py:183-197``)."""
 
     def __init__(self, inputs: int, outputs: int) -> None:
         super().__init__()
@@ -82,9 +83,9 @@ def _lengths_from_blocked_mask(mask: Tensor, chunk: int, past: int) -> Tensor:
 
 
 class AudioAttention(nn.Module):
-    """Local attention over blocks of ``chunk`` frames: each frame sees itself
-    and the ``past - 1`` frames before it, with a relative position bias
-    (``gemma4.py:199-282``)."""
+    """Gemma 4's audio attention (``gemma4.py:199-282``): frames are grouped
+    in blocks of ``chunk``; a frame attends to itself and its ``past - 1``
+    predecessors, scores get a learned bias by relative distance."""
 
     def __init__(self, config: dict) -> None:
         super().__init__()
@@ -107,8 +108,9 @@ class AudioAttention(nn.Module):
         self.per_dim_scale = nn.Parameter(torch.zeros(self.head_dim))
 
     def blocked_mask(self, lengths: Tensor, frames: int) -> Tensor:
-        """``(batch, 1, blocks, chunk, context)``, True where a query must not
-        attend (``gemma4.py:223-240``)."""
+        """The blocked layout's exclusion mask (``gemma4.py:223-240``): shape
+        ``(batch, 1, blocks, chunk, context)``, True for each (query, context
+        slot) pair that is out of reach or past the sequence's length."""
         blocks = -(-frames // self.chunk)
         device = lengths.device
         query = torch.arange(blocks * self.chunk, device=device).view(blocks, self.chunk, 1)
@@ -144,8 +146,9 @@ class AudioAttention(nn.Module):
 
 
 def rotate(x: Tensor, cos: Tensor, sin: Tensor) -> Tensor:
-    """Rotary embedding of ``(..., heads, head_dim)`` with ``cos``/``sin``
-    ``(..., head_dim)`` (``gemma4.py:440-445``)."""
+    """Half-split rotary embedding (``gemma4.py:440-445``): ``x`` is
+    ``(..., heads, head_dim)``; ``cos`` and ``sin`` are ``(..., head_dim)``,
+    broadcast over the heads."""
     first, second = x.chunk(2, dim=-1)
     rotated = torch.cat((-second, first), dim=-1)
     return x * cos[..., None, :] + rotated * sin[..., None, :]
@@ -170,8 +173,8 @@ def rotary_tables(text: dict, layer_type: str, head_dim: int, length: int) -> tu
 
 @dataclass
 class LayerKV:
-    """Preallocated keys and values of a layer, ``(batch, length, kv_heads,
-    head_dim)``, written in place (``gemma4.py:469-483``)."""
+    """One layer's cache tensors, ``(batch, length, kv_heads, head_dim)``,
+    allocated once and updated in place (``gemma4.py:469-483``)."""
 
     keys: Tensor
     values: Tensor
@@ -187,9 +190,10 @@ def _prompt_sizes(mask: Tensor) -> Tensor:
 
 
 class TextAttention(nn.Module):
-    """Attention with query/key/value norms and no scaling; layers in the last
-    ``num_kv_shared_layers`` read the keys and values of the last earlier
-    layer of their type (``gemma4.py:486-587``)."""
+    """Gemma 4's text attention (``gemma4.py:486-587``): RMS norms on the
+    queries, keys and values, softmax without a 1/sqrt(d) factor.  The final
+    ``num_kv_shared_layers`` layers project queries only and reuse the cache
+    of the nearest earlier layer of the same kind."""
 
     def __init__(self, text: dict, layer_type: str, shared: bool) -> None:
         super().__init__()
@@ -225,9 +229,10 @@ class TextAttention(nn.Module):
 
     def prefill(self, x: Tensor, cache: LayerKV, rows: Tensor, kv: dict[str, tuple[Tensor, Tensor]],
                 mask: Tensor | KeyPrefix, cos: Tensor, sin: Tensor) -> Tensor:
-        """Attention over padded prompts ``x`` (batch, length, width) written to
-        ``rows`` of the cache; ``mask`` is the prompt pass's (causal, each
-        prompt's size, the window) or a :class:`KeyPrefix` of the sizes."""
+        """The prompt pass: padded prompts ``x`` ``(batch, length, width)``
+        attend causally (within the window on sliding layers) and their keys
+        and values go to cache ``rows``.  ``mask`` is either the reference's
+        prompt mask or a :class:`KeyPrefix` holding each prompt's size."""
         q, k, v = self._project(x, cos, sin)
         if self.shared:
             k, v = kv[self.layer_type]

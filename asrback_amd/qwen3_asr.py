@@ -66,8 +66,9 @@ class Segments:
 
 
 def attend(q: Tensor, k: Tensor, v: Tensor, segments: Segments, causal: bool) -> Tensor:
-    """Attention within each segment of packed ``(tokens, heads, head_dim)``
-    tensors; ``k``/``v`` may have fewer heads (``qwen3_asr.py:152-181``)."""
+    """``varlen_attn`` over packed ``(tokens, heads, head_dim)`` segments
+    (``qwen3_asr.py:152-181``), grouped-query when ``k``/``v`` carry fewer
+    heads than ``q``."""
     return varlen_attn(
         q,
         k,
@@ -108,8 +109,9 @@ class RMSNorm(nn.Module):
 
 
 def rotate(x: Tensor, cos: Tensor, sin: Tensor) -> Tensor:
-    """Half-split rotary embedding of ``(..., heads, head_dim)`` with
-    ``cos``/``sin`` ``(..., head_dim)`` (``qwen3_asr.py:326-330``)."""
+    """RoPE in the half-split convention (``qwen3_asr.py:326-330``): ``x``
+    ``(..., heads, head_dim)``, tables ``(..., head_dim)`` shared by the
+    heads."""
     first, second = x.chunk(2, dim=-1)
     rotated = torch.cat((-second, first), dim=-1)
     return x * cos[..., None, :] + rotated * sin[..., None, :]
@@ -127,9 +129,10 @@ def rope_tables(config: dict, length: int, device: torch.device, dtype: torch.dt
 
 @dataclass
 class KVCache:
-    """Preallocated keys and values, ``(layers, batch, length, kv_heads,
-    head_dim)`` (``qwen3_asr.py:333-347``); written in place, so the tensors
-    keep fixed addresses across graph replays."""
+    """The slab cache (``qwen3_asr.py:333-347``): one
+    ``(layers, batch, length, kv_heads, head_dim)`` tensor each for keys and
+    values, allocated once; every write is in place, so captured graphs keep
+    valid addresses."""
 
     keys: Tensor
     values: Tensor
@@ -149,7 +152,9 @@ class PagedLayer:
     positions] = x`` writes each token to its row's page."""
 
     def __init__(self, pool: Tensor, table: PageTable, page_size: int) -> None:
-        self.pool = pool  # (num_pages, page_size, kv_heads, head_dim)
+        # (num_pages + 1, page_size, kv_heads, head_dim): the last page is a
+        # sink that no table entry names.
+        self.pool = pool
         self.table = table
         self.page_size = page_size
         self.dtype = pool.dtype
@@ -160,13 +165,19 @@ class PagedLayer:
     def __setitem__(self, index: tuple[Tensor, Tensor], value: Tensor) -> None:
         rows, positions = index
         pages = self.table.block_table[rows, positions // self.page_size].long()
+        # A row without a page there (-1: a free row of the bucket) writes to
+        # the sink page, so it cannot land in a page another row owns; no
+        # data-dependent shapes, so the write can be graph-captured.
+        sink = self.pool.shape[0] - 1
+        pages = torch.where((pages >= 0) & (pages < sink), pages, sink)
         self.pool[pages, positions % self.page_size] = value
 
 
 @dataclass
 class PagedKVCache:
     """Keys and values in pages of ``page_size`` positions from one pool per
-    layer, ``(layers, num_pages, page_size, kv_heads, head_dim)``, and a block
+    layer, ``(layers, num_pages + 1, page_size, kv_heads, head_dim)`` (the
+    last page a write sink that no row owns), and a block
     table ``(batch, CACHE_LENGTH / page_size)`` (int32, on the device; -1 for
     no page) mapping each row's logical pages to pool pages.  Generalizes the
     reference's ``row * 1024`` slab (``qwen3_asr.py:511-512``): a row holds
@@ -184,7 +195,9 @@ class PagedKVCache:
     def allocate(cls, config: dict, batch: int, num_pages: int, page_size: int, device, dtype) -> PagedKVCache:
         if CACHE_LENGTH % page_size:
             raise ValueError(f"page_size must divide {CACHE_LENGTH}")
-        shape = (config["num_hidden_layers"], num_pages, page_size, config["num_key_value_heads"], config["head_dim"])
+        # One page more than the table hands out: the sink of PagedLayer.
+        shape = (config["num_hidden_layers"], num_pages + 1, page_size, config["num_key_value_heads"],
+                 config["head_dim"])
         table = torch.full((batch, CACHE_LENGTH // page_size), -1, dtype=torch.int32, device=device)
         return cls(torch.zeros(shape, dtype=dtype, device=device), torch.zeros(shape, dtype=dtype, device=device),
                    table, page_size, list(range(num_pages - 1, -1, -1)))
@@ -263,8 +276,9 @@ class TextAttention(nn.Module):
         return q, k, v.reshape(shape)
 
     def prefill(self, x, keys, values, rows, positions, segments: Segments, cos, sin) -> Tensor:
-        """Causal attention within each packed prompt; every token's key and
-        value go to its row and position of the cache (``:374-390``)."""
+        """The prompt pass (``:374-390``): keys and values of the packed
+        prompts are stored at (row, position) in the cache, then each prompt
+        attends causally within itself."""
         q, k, v = self._project(x, cos, sin)
         keys[rows, positions] = k
         values[rows, positions] = v
@@ -374,7 +388,7 @@ class DecodeState:
 
     tokens: Tensor  # (batch,)
     position: Tensor  # (batch,)
-    end: Tensor  # (batch,), the last position a row may write
+    end: Tensor  # (batch,): each row's final writable position
     finished: Tensor  # (batch,)
     sum_logprobs: Tensor  # (batch,)
     generated: Tensor  # (batch, CACHE_LENGTH)
@@ -396,7 +410,8 @@ class DecodeState:
         )))
 
     def free(self, rows: Tensor) -> None:
-        """Mark ``rows`` free: finished, at position 0."""
+        """Return ``rows`` to the pool of free slots (finished, back at
+        position 0)."""
         self.finished[rows] = True
         self.position[rows] = 0
         self.tokens[rows] = 0

@@ -11,6 +11,15 @@ expressed as ``seqused_k = lengths``: the reference's ``varlen_attn`` path
 masked depthwise convolution (``:99-107``) become one launch, and
 ``linear_out(attention) + memory`` one GEMM accumulating into the memory
 (which carries ``linear_out``'s bias).
+
+Padded frames: the attention of a padded frame (a query at or past its
+row's length) is not computed; it is zero, so that frame's output is
+``linear_out``'s bias alone.  No valid frame can see the difference: every
+later op on a padded frame is row-local (norms, linear layers, the FFN), the
+FSMN convolution reads values through the frame mask (``sensevoice.py:99-107``:
+padded frames contribute zeros) and attention reads keys ``0 .. n_b - 1`` only
+(``:115-125``).  Valid frames are bit-identical with or without the skip
+(``SANMAttention.zero_padded_rows``).
 """
 
 from __future__ import annotations
@@ -27,6 +36,10 @@ from .attention import flash_fsmn
 class SANMAttention(nn.Module):
     """Self-attention plus a depthwise convolution (FSMN memory) over the
     values (``sensevoice.py:66-135``)."""
+
+    # Padded frames' attention rows are zeros instead of computed (see the
+    # module docstring); valid frames are unchanged.
+    zero_padded_rows = True
 
     def __init__(self, in_size: int, size: int, heads: int, kernel_size: int) -> None:
         super().__init__()
@@ -56,6 +69,7 @@ class SANMAttention(nn.Module):
             self.fsmn_block.weight,
             seqused_k=lengths,
             bias=self.linear_out.bias,
+            zero_padded_rows=self.zero_padded_rows and lengths is not None,
         )
         # linear_out(output) + memory: the bias is in memory already.
         memory.view(-1, self.size).addmm_(output.view(-1, self.size), self.linear_out.weight.t())

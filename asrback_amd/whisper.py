@@ -30,11 +30,11 @@ import torch
 import torch.nn.functional as F
 from torch import Tensor, nn
 
-from .attention import KeyPrefix, greedy_choice, sdpa
+from .attention import KeyPrefix, decode_append, greedy_choice, sdpa
 from .transcription import CapturedGraph, to_device
 
-# Self-attention lengths with their own graph, besides max_target_positions
-# (whisper.py:54).
+# Key buckets of the graphed decoder step; max_target_positions is the last
+# one (whisper.py:54).
 KV_BUCKETS = (64, 128, 256)
 # Decoder steps between host checks for finished rows (whisper.py:52).
 EOS_CHECK_INTERVAL = 4
@@ -59,8 +59,21 @@ class MultiHeadAttention(nn.Module):
         return x.view(batch, length, self.heads, width // self.heads).transpose(1, 2)
 
     def project_key_value(self, x: Tensor) -> tuple[Tensor, Tensor]:
-        """``(batch, heads, length, head_dim)`` keys and values for ``x``."""
+        """Keys and values of ``x`` as ``(batch, heads, length, head_dim)``
+        views of the projections (no copy)."""
         return self._split_heads(self.k_proj(x)), self._split_heads(self.v_proj(x))
+
+    def step(self, x: Tensor, key: Tensor, value: Tensor, keys: Tensor, values: Tensor, positions: Tensor) -> Tensor:
+        """One query token per row (``x`` ``(batch, 1, width)``) whose own key
+        and value (``(batch, heads, 1, head_dim)``) go into the self-attention
+        cache ``keys``/``values`` ``(batch, heads, length, head_dim)`` at
+        ``positions`` before the row attends keys ``0 .. positions[b]``: the
+        reference's ``scatter_`` pair and masked SDPA (``whisper.py:224-237``)
+        as one ``decode_append`` launch."""
+        query = self._split_heads(self.q_proj(x))[:, :, 0]
+        output = decode_append(query, key[:, :, 0], value[:, :, 0], keys.transpose(1, 2), values.transpose(1, 2),
+                               positions)
+        return self.out_proj(output.reshape(x.shape[0], 1, -1))
 
     def attend(
         self,
@@ -75,7 +88,7 @@ class MultiHeadAttention(nn.Module):
         return self.out_proj(output.reshape(x.shape[0], x.shape[1], -1))
 
     def forward(self, x: Tensor) -> Tensor:
-        """Unmasked self-attention."""
+        """Self-attention of ``x`` over itself, no mask (the encoder's)."""
         return self.attend(x, *self.project_key_value(x))
 
 
@@ -123,9 +136,9 @@ class WhisperEncoder(nn.Module):
 
 @dataclass
 class DecoderCache:
-    """Preallocated keys and values, ``(layers, batch, heads, length, head_dim)``
-    (``whisper.py:156-196``).  Entries are written in place, so the tensors keep
-    fixed addresses across graph replays."""
+    """Self- and cross-attention caches, ``(layers, batch, heads, length,
+    head_dim)`` each (``whisper.py:156-196``), allocated once and updated in
+    place so that captured graphs keep valid addresses."""
 
     self_keys: Tensor
     self_values: Tensor
@@ -183,18 +196,26 @@ class DecoderLayer(nn.Module):
         self_keys, self_values, cross_keys, cross_values = cache
         hidden = self.self_attn_layer_norm(x)
         key, value = self.self_attn.project_key_value(hidden)
-        if length is None:
-            # Fixed-shape step: one token per row, each at its own position.
-            index = positions[:, None, None, None].expand_as(key)
-            self_keys.scatter_(2, index, key)
-            self_values.scatter_(2, index, value)
+        if length is None and isinstance(mask, KeyPrefix) and mask.positions is positions:
+            # The graphed step (one token per row, rows at different
+            # positions, each seeing keys up to its own): cache write and
+            # attention in one launch.
+            x = x + self.self_attn.step(hidden, key, value, self_keys, self_values, positions)
         else:
-            # Eager: tokens at shared positions; attend to the filled prefix.
-            self_keys.index_copy_(2, positions, key)
-            self_values.index_copy_(2, positions, value)
-            self_keys = self_keys[:, :, :length]
-            self_values = self_values[:, :, :length]
-        x = x + self.self_attn.attend(hidden, self_keys, self_values, mask=mask, is_causal=x.shape[1] > 1)
+            if length is None:
+                # Per-row positions with another mask form: write each row's
+                # token at its own position, then attend as the mask says.
+                index = positions[:, None, None, None].expand_as(key)
+                self_keys.scatter_(2, index, key)
+                self_values.scatter_(2, index, value)
+            else:
+                # Prompt pass: every row writes the same positions and attends
+                # causally over the prefix written so far.
+                self_keys.index_copy_(2, positions, key)
+                self_values.index_copy_(2, positions, value)
+                self_keys = self_keys[:, :, :length]
+                self_values = self_values[:, :, :length]
+            x = x + self.self_attn.attend(hidden, self_keys, self_values, mask=mask, is_causal=x.shape[1] > 1)
         hidden = self.encoder_attn_layer_norm(x)
         x = x + self.encoder_attn.attend(hidden, cross_keys, cross_values)
         return x + self.fc2(F.gelu(self.fc1(self.final_layer_norm(x))))
@@ -214,8 +235,8 @@ class WhisperDecoder(nn.Module):
     def forward(self, tokens: Tensor, positions: Tensor, cache: DecoderCache, length: int | None) -> Tensor:
         mask = None
         if length is None:
-            # Fixed-shape step over the whole cache view, one position per row:
-            # row b sees keys 0..positions[b] (read on the device).
+            # Graphed step over the bucket's cache view: row b is at
+            # positions[b] and sees keys 0 .. positions[b] (read on the device).
             x = self.embed_tokens(tokens) + self.embed_positions(positions)[:, None]
             mask = KeyPrefix(positions=positions)
         else:

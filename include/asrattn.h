@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define ASRATTN_ABI_VERSION 9
+#define ASRATTN_ABI_VERSION 10
 
 enum asrattn_status {
   ASRATTN_OK = 0,
@@ -47,6 +47,12 @@ enum asrattn_dtype { ASRATTN_F32 = 0, ASRATTN_BF16 = 1 };
 /* asrattn_fwd_params.flags: run the fp32 vector-ALU kernel even where the
    bf16 matrix-core kernel applies (the exact-arithmetic twin, for checks). */
 #define ASRATTN_FWD_FORCE_VALU 1
+/* asrattn_fwd_params.flags: padded layout (cu_seqlens NULL), non-causal,
+   seqused_k given: query rows t >= seqused_k[b] are not computed and get
+   zeros.  Rows t < seqused_k[b] are unchanged.  For callers whose padded
+   rows never reach a valid row (SenseVoice's encoder: every later op on a
+   padded frame is row-local or masked, sensevoice.py:97-107, :115-125). */
+#define ASRATTN_FWD_ZERO_PADDED_ROWS 2
 
 enum asrattn_causal {
   ASRATTN_CAUSAL_NONE = 0,
@@ -107,7 +113,7 @@ typedef struct asrattn_fwd_params {
   int32_t causal; /* enum asrattn_causal */
   int32_t dtype;  /* enum asrattn_dtype */
   float scale;    /* softmax scale; torch's default is 1 / sqrt(head_dim) */
-  int32_t flags;  /* 0, or ASRATTN_FWD_FORCE_VALU */
+  int32_t flags;  /* 0 or a combination of ASRATTN_FWD_* flags */
   int32_t window; /* > 0 (causal only): query i also sees no key more than
                      window - 1 before its last visible one (sliding-window
                      attention, gemma4.py:1231-1234); 0: none */

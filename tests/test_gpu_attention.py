@@ -13,12 +13,13 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import GOLDEN, max_rel_err
+from conftest import GOLDEN, assert_close, max_rel_err
 from oracle import attention as oa
 
 pytestmark = pytest.mark.gpu
 
 TOL = {torch.float32: 1e-5, torch.bfloat16: 2e-2}
+KIND = {torch.float32: "f32", torch.bfloat16: "bf16"}  # tolerance classes of conftest.assert_close
 DTYPES = [torch.float32, torch.bfloat16]
 
 
@@ -51,7 +52,7 @@ def test_encoder_golden(golden, ops, device, dtype, force_valu):
     say("encoder golden", dtype, force_valu)
     q, k, v = (dev(golden[f"enc_{n}"], dtype, device) for n in "qkv")
     out = ops.flash(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), force_valu=force_valu)
-    assert max_rel_err(out.transpose(1, 2), golden["enc_out"]) < TOL[dtype]
+    assert_close(out.transpose(1, 2), golden["enc_out"], KIND[dtype])
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
@@ -62,7 +63,7 @@ def test_prefix_golden(golden, ops, device, dtype, force_valu):
     out = ops.flash(
         q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), causal=1, force_valu=force_valu
     )
-    assert max_rel_err(out.transpose(1, 2), golden["prefix_out"]) < TOL[dtype]
+    assert_close(out.transpose(1, 2), golden["prefix_out"], KIND[dtype])
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
@@ -71,11 +72,11 @@ def test_step_golden(golden, ops, device, dtype):
     q, k, v = (dev(golden[f"step_{n}"], dtype, device) for n in "qkv")
     positions = torch.from_numpy(golden["step_positions"]).to(device)
     out = ops.sdpa(q, k, v, ops.KeyPrefix(positions=positions))  # (B, 1, H, D)
-    assert max_rel_err(out.transpose(1, 2), golden["step_out"]) < TOL[dtype]
+    assert_close(out.transpose(1, 2), golden["step_out"], KIND[dtype])
     # The boolean mask the reference builds gives the same result.
     mask = oa.whisper_step_mask(positions, k.shape[2])
     out2 = ops.sdpa(q, k, v, mask)
-    assert max_rel_err(out2.transpose(1, 2), golden["step_out"]) < TOL[dtype]
+    assert_close(out2.transpose(1, 2), golden["step_out"], KIND[dtype])
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
@@ -83,7 +84,7 @@ def test_cross_golden(golden, ops, device, dtype):
     say("cross golden", dtype)
     q, k, v = (dev(golden[f"cross_{n}"], dtype, device) for n in "qkv")
     out = ops.sdpa(q, k, v)
-    assert max_rel_err(out.transpose(1, 2), golden["cross_out"]) < TOL[dtype]
+    assert_close(out.transpose(1, 2), golden["cross_out"], KIND[dtype])
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
@@ -95,7 +96,7 @@ def test_padded_golden(golden, ops, device, dtype, force_valu):
     out = ops.flash(
         q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), seqused_k=lengths, force_valu=force_valu
     )
-    assert max_rel_err(out.transpose(1, 2), golden["padded_out"]) < TOL[dtype]
+    assert_close(out.transpose(1, 2), golden["padded_out"], KIND[dtype])
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
@@ -109,7 +110,7 @@ def test_packed_gqa_golden(golden, ops, device, dtype, force_valu):
         q, k, v, causal=2, cu_seqlens_q=starts, cu_seqlens_k=starts,
         max_len_q=longest, max_len_k=longest, force_valu=force_valu,
     )
-    assert max_rel_err(out, golden["packed_out"]) < TOL[dtype]
+    assert_close(out, golden["packed_out"], KIND[dtype])
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
@@ -118,4 +119,4 @@ def test_gqa_step_golden(golden, ops, device, dtype):
     q, k, v = (dev(golden[f"gqa_step_{n}"], dtype, device) for n in "qkv")
     used = torch.from_numpy(golden["gqa_step_used"]).to(device)
     out = ops.decode(q, k, v, seqused_k=used)
-    assert max_rel_err(out, golden["gqa_step_out"]) < TOL[dtype]
+    assert_close(out, golden["gqa_step_out"], KIND[dtype])

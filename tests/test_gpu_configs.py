@@ -12,12 +12,13 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import max_rel_err
+from conftest import assert_close, max_rel_err
 from oracle import attention as oa
 
 pytestmark = pytest.mark.gpu
 
 TOL = {torch.float32: 1e-5, torch.bfloat16: 2e-2}
+KIND = {torch.float32: "f32", torch.bfloat16: "bf16"}  # tolerance classes of conftest.assert_close
 
 
 @pytest.fixture(scope="module")
@@ -53,7 +54,7 @@ def test_sensevoice_ragged_batch(ops, device, dtype):
     x = fused.to(device)
     q, k, v = (t.view(32, length, 4, 128) for t in x.split(512, dim=-1))
     out = ops.flash(q, k, v, seqused_k=lengths.to(device))
-    assert max_rel_err(out.reshape(32, length, 512), ref) < TOL[dtype]
+    assert_close(out.reshape(32, length, 512), ref, KIND[dtype])
 
 
 def test_sensevoice_unmasked_equals_masked_full_length(ops, device):
@@ -94,7 +95,7 @@ def test_sensevoice_fsmn_fused_matches_oracle(ops, device, dtype):
     out, memory = ops.flash_fsmn(q, k, v, weight.to(device), seqused_k=used, bias=bias.to(device))
     assert torch.equal(out, ops.flash(q, k, v, seqused_k=used))
     ref = _fsmn_reference(fused, 4, lengths, weight, bias)
-    assert max_rel_err(memory.cpu(), ref) < TOL[dtype]
+    assert_close(memory.cpu(), ref, KIND[dtype])
     for b in (int(lengths.argmin()), 0):
         n = int(lengths[b])
         assert torch.equal(memory[b, n:].cpu(), bias.expand(length - n, 512))
@@ -131,15 +132,15 @@ def test_fsmn_kernel_sizes_and_edges(ops, device, dtype, heads, head_dim, kernel
         q, k, v, weight.to(device), seqused_k=lengths.to(device), force_valu=force_valu
     )
     ref = _fsmn_reference(fused, heads, lengths, weight, None)
-    assert max_rel_err(memory.cpu(), ref) < TOL[dtype]
+    assert_close(memory.cpu(), ref, KIND[dtype])
     assert not memory[3].any() and not memory[2, 2:].any()
     # (the frame-less row's reference is NaN: softmax over no keys)
     valid = oa.key_padding_mask(lengths, 130)
     attention = oa.sensevoice_attention(fused.float(), heads, valid)
-    assert max_rel_err(out.reshape(4, 130, width).cpu()[valid], attention[valid]) < TOL[dtype]
+    assert_close(out.reshape(4, 130, width).cpu()[valid], attention[valid], KIND[dtype])
     # Without frame counts every frame is real.
     _, full = ops.flash_fsmn(q, k, v, weight.to(device), force_valu=force_valu)
-    assert max_rel_err(full.cpu(), _fsmn_reference(fused, heads, None, weight, None)) < TOL[dtype]
+    assert_close(full.cpu(), _fsmn_reference(fused, heads, None, weight, None), KIND[dtype])
 
 
 def test_fsmn_fused_epilogue_equals_separate_kernel(ops, device):
@@ -169,7 +170,7 @@ def test_whisper_encoder_shapes(ops, device, dtype):
     xd = x.to(device)
     qd, kd, vd = (oa.split_heads(t, heads) for t in xd.split(heads * 64, dim=-1))
     out = ops.sdpa(qd, kd, vd)  # (B, L, H, D)
-    assert max_rel_err(out.transpose(1, 2), ref) < TOL[dtype]
+    assert_close(out.transpose(1, 2), ref, KIND[dtype])
 
 
 @pytest.mark.parametrize("length", [1, 2, 31, 63, 64, 65, 127, 129, 448])
@@ -179,7 +180,7 @@ def test_causal_prefix_lengths(ops, device, length):
     q, k, v = (randn(3, 6, length, 64, seed=14 + i, dtype=torch.bfloat16) for i in range(3))
     ref = oa.sdpa(q.float(), k.float(), v.float(), is_causal=length > 1)
     out = ops.sdpa(q.to(device), k.to(device), v.to(device), is_causal=length > 1)
-    assert max_rel_err(out.transpose(1, 2), ref) < 2e-2
+    assert_close(out.transpose(1, 2), ref, "bf16")
 
 
 def test_qwen_packed_causal_prefill(ops, device):
@@ -195,7 +196,7 @@ def test_qwen_packed_causal_prefill(ops, device):
     starts = segments.starts.to(device)
     out = ops.varlen_attn(q.to(device), k.to(device), v.to(device), starts, starts, max(lengths),
                           max(lengths), window_size=(-1, 0), enable_gqa=True)
-    assert max_rel_err(out, ref) < 2e-2
+    assert_close(out, ref, "bf16")
 
 
 def test_qwen_audio_windows_noncausal(ops, device):
@@ -208,7 +209,7 @@ def test_qwen_audio_windows_noncausal(ops, device):
     ref = oa.qwen_attend(q.float(), k.float(), v.float(), segments, causal=False)
     starts = segments.starts.to(device)
     out = ops.varlen_attn(q.to(device), k.to(device), v.to(device), starts, starts, 104, 104)
-    assert max_rel_err(out, ref) < 2e-2
+    assert_close(out, ref, "bf16")
 
 
 # --- decoder steps ---------------------------------------------------------------
@@ -233,8 +234,8 @@ def test_whisper_small_decoder_step(ops, device, dtype):
     qd, kd, vd = q.to(device), cache_k.to(device), cache_v.to(device)
     out_self = ops.sdpa(qd, kd[:, :, :256], vd[:, :, :256], ops.KeyPrefix(positions=positions.to(device)))
     out_cross = ops.sdpa(qd, cross_k.to(device), cross_v.to(device))
-    assert max_rel_err(out_self.transpose(1, 2), ref_self) < TOL[dtype]
-    assert max_rel_err(out_cross.transpose(1, 2), ref_cross) < TOL[dtype]
+    assert_close(out_self.transpose(1, 2), ref_self, KIND[dtype])
+    assert_close(out_cross.transpose(1, 2), ref_cross, KIND[dtype])
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
@@ -251,7 +252,7 @@ def test_qwen_gqa_decode(ops, device, dtype):
     ref = oa.qwen_step_attention(q.float(), keys.float(), values.float(), oa.qwen_step_mask(positions, 1024))
     used = (positions + 1).to(torch.int32).to(device)
     out = ops.decode(q.to(device), keys.to(device), values.to(device), seqused_k=used)
-    assert max_rel_err(out, ref) < TOL[dtype]
+    assert_close(out, ref, KIND[dtype])
 
 
 @pytest.mark.parametrize("splits", [1, 2, 3, 7, 16, 64])
@@ -301,7 +302,7 @@ def test_decode_ignores_cache_slots_past_each_row(ops, device, dtype, hd, heads_
     out = ops.decode(q.to(device), keys_nan.to(device), values_nan.to(device), seqused_k=used,
                      num_splits=splits).float().cpu()
     assert torch.count_nonzero(out[0]) == 0
-    assert max_rel_err(out[1:], ref[1:]) < TOL[dtype]
+    assert_close(out[1:], ref[1:], KIND[dtype])
 
     # Append: row b's step key goes to slot n_b and attends keys 0..n_b.
     positions = n.clone()
@@ -315,7 +316,7 @@ def test_decode_ignores_cache_slots_past_each_row(ops, device, dtype, hd, heads_
     kd, vd = keys_nan.to(device), values_nan.to(device)
     out = ops.decode_append(q.to(device), k_new.to(device), v_new.to(device), kd, vd, positions.to(device),
                             num_splits=splits)
-    assert max_rel_err(out.float().cpu(), ref) < TOL[dtype]
+    assert_close(out.float().cpu(), ref, KIND[dtype])
     assert torch.equal(kd.cpu()[rows, positions], k_new) and torch.equal(vd.cpu()[rows, positions], v_new)
 
 
@@ -334,7 +335,7 @@ def test_step_matches_last_row_of_prefill_on_gpu(ops, device):
     for p in (0, 17, 39):
         pos = torch.full((2,), p, dtype=torch.int64, device=device)
         step = ops.sdpa(q[:, :, p : p + 1], k, v, ops.KeyPrefix(positions=pos))
-        assert max_rel_err(step[:, 0].float(), full[:, p].float()) < 2e-2
+        assert_close(step[:, 0].float(), full[:, p].float(), "bf16")
 
 
 def test_decode_replays_from_a_graph(ops, device):
@@ -428,7 +429,7 @@ def test_decode_append_matches_oracle(ops, device, dtype, batch, heads_q, heads_
     out = ops.decode_append(q.to(device), k_new.to(device), v_new.to(device), kd, vd, positions.to(device),
                             q_norm=q_w.to(device), k_norm=k_w.to(device), eps=eps, cos=cos.to(device),
                             sin=sin.to(device), num_splits=splits)
-    assert max_rel_err(out, ref) < TOL[dtype]
+    assert_close(out, ref, KIND[dtype])
     assert _ulp_diff_ok(kd.cpu()[rows, positions], kn, dtype)
     assert torch.equal(vd.cpu()[rows, positions], v_new)
     untouched = torch.ones(batch, length, dtype=torch.bool)
@@ -479,7 +480,7 @@ def test_decode_append_gemma_prologue_matches_oracle(ops, device, dtype):
     out = ops.decode_append(q.to(device), k_new.to(device), v_new.to(device), kd, vd, positions.to(device),
                             q_norm=q_w.to(device), k_norm=k_w.to(device), eps=eps, cos=cos.to(device),
                             sin=sin.to(device), scale=1.0, window=window, v_norm=True)
-    assert max_rel_err(out, ref) < TOL[dtype]
+    assert_close(out, ref, KIND[dtype])
     assert _ulp_diff_ok(kd.cpu()[rows, positions], kn, dtype)
     assert _ulp_diff_ok(vd.cpu()[rows, positions], vn, dtype)
 
@@ -545,7 +546,7 @@ def test_paged_decode_matches_slab_and_oracle(ops, device, dtype, hd, heads_q, h
     out = ops.decode(q.to(device), pool_k.to(device), pool_v.to(device), seqused_k=used.to(device),
                      num_splits=splits, pages=pages)
     assert torch.isfinite(out).all()
-    assert max_rel_err(out, ref) < TOL[dtype]
+    assert_close(out, ref, KIND[dtype])
     if batch == 64:
         slab = ops.decode(q.to(device), keys.to(device), values.to(device), seqused_k=used.to(device))
         assert torch.equal(out, slab)
@@ -633,7 +634,7 @@ def test_gemma_decode_window_and_head_sizes(ops, device, dtype, hd, heads_q, hea
         out = ops.decode(q.to(device), keys.to(device), values.to(device), seqused_k=used, scale=1.0,
                          window=window, num_splits=splits)
     assert torch.isfinite(out).all()
-    assert max_rel_err(out, ref) < TOL[dtype]
+    assert_close(out, ref, KIND[dtype])
 
 
 @pytest.mark.parametrize(
@@ -668,7 +669,7 @@ def test_gemma_prefill_window_and_head_sizes(ops, device, dtype, hd, heads_q, he
     out = ops.flash(q.to(device), k.to(device), v.to(device), causal=1, seqused_k=sizes.int().to(device),
                     scale=1.0, window=window).cpu()
     for b, n in enumerate(sizes.tolist()):
-        assert max_rel_err(out[b, :n], ref[b, :n]) < TOL[dtype]
+        assert_close(out[b, :n], ref[b, :n], KIND[dtype])
 
 
 def test_gemma_decode_append_window(ops, device):
@@ -693,7 +694,7 @@ def test_gemma_decode_append_window(ops, device):
     kd, vd = keys.to(device), values.to(device)
     out = ops.decode_append(q.to(device), k_new.to(device), v_new.to(device), kd, vd, positions.to(device),
                             scale=1.0, window=window)
-    assert max_rel_err(out, ref.reshape(batch, heads_q, hd)) < TOL[torch.bfloat16]
+    assert_close(out, ref.reshape(batch, heads_q, hd), KIND[torch.bfloat16])
     assert torch.equal(kd.cpu()[rows, positions], k_new) and torch.equal(vd.cpu()[rows, positions], v_new)
 
 
@@ -718,7 +719,7 @@ def test_decode_append_whisper_cache_without_norm(ops, device):
     kd, vd = cache_k.to(device), cache_v.to(device)
     out = ops.decode_append(q.to(device), k_new.to(device), v_new.to(device), kd[:, :, :256].transpose(1, 2),
                             vd[:, :, :256].transpose(1, 2), positions.to(device))
-    assert max_rel_err(out, ref) < TOL[torch.bfloat16]
+    assert_close(out, ref, KIND[torch.bfloat16])
     assert torch.equal(kd.cpu(), ref_k) and torch.equal(vd.cpu(), ref_v)
 
 
@@ -787,3 +788,14 @@ def test_greedy_choice_column_major_logits(ops, device):
     got_t, got_p = ops.greedy_choice(logits)
     assert torch.equal(got_t.cpu(), want_t)
     assert torch.allclose(got_p.cpu(), want_p, rtol=1e-5, atol=1e-5)
+
+
+def test_flash_refuses_out_without_unit_last_stride(ops, device):
+    """The forward kernels write each head's head_dim elements contiguously:
+    an out view with a non-unit last stride is refused, not written wrongly."""
+    q = randn(1, 4, 2, 64, seed=30, dtype=torch.bfloat16).to(device)
+    out = torch.zeros(1, 4, 2, 128, dtype=torch.bfloat16, device=device)[..., ::2]
+    with pytest.raises(ValueError, match="unit last stride"):
+        ops.flash(q, q, q, out=out)
+    with pytest.raises(ValueError, match="unit last stride"):
+        ops.flash_fsmn(q, q, q, torch.zeros(128, 11, dtype=torch.bfloat16, device=device), out=out)

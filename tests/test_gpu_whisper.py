@@ -16,7 +16,7 @@ import json
 import pytest
 import torch
 
-from conftest import GOLDEN, max_rel_err
+from conftest import GOLDEN, assert_close, max_rel_err
 from oracle import whisper as ow
 
 pytestmark = pytest.mark.gpu
@@ -96,7 +96,7 @@ def test_encoder_and_prefix_hidden_states_match_oracle(fixture, weights, device)
     with torch.inference_mode():
         enc_ref = ref.model.encoder(mel)
         enc = model.model.encoder(mel.to(device))
-        assert max_rel_err(enc.cpu(), enc_ref) < 1e-4
+        assert_close(enc.cpu(), enc_ref, "module", 1e-4)
         cache_ref = ref.allocate_cache(1)
         ref.set_encoder_output(cache_ref, enc_ref)
         prefix = torch.tensor([fixture["prefix"]])
@@ -104,7 +104,7 @@ def test_encoder_and_prefix_hidden_states_match_oracle(fixture, weights, device)
         cache = model.allocate_cache(1)
         model.set_encoder_output(cache, enc)
         hid = model.decode(prefix.to(device), torch.arange(4, device=device), cache, length=4)
-        assert max_rel_err(hid.cpu(), hid_ref) < 1e-4
+        assert_close(hid.cpu(), hid_ref, "module", 1e-4)
 
 
 def test_bf16_model_decodes(fixture, weights, device):

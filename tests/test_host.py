@@ -31,6 +31,15 @@ def test_key_prefix_validation_and_mask_conversion():
     assert prefix.lengths.tolist() == [1, 5, 10]
     with pytest.raises(TypeError):
         KeyPrefix.from_mask(mask.float())
+    # A hole (False before True) is not a prefix: refused, not reduced to a count.
+    holed = mask.clone()
+    holed[2, 3] = False
+    with pytest.raises(ValueError, match="prefix"):
+        KeyPrefix.from_mask(holed[:, None, None, :])
+    # Masks with more than one query row per sequence are not key prefixes.
+    with pytest.raises(ValueError, match="mask"):
+        KeyPrefix.from_mask(torch.ones(3, 1, 2, 10, dtype=torch.bool))
+    assert KeyPrefix.from_mask(torch.zeros(2, 5, dtype=torch.bool)).lengths.tolist() == [0, 0]
 
 
 def test_ops_refuse_cpu_tensors_instead_of_falling_back():
@@ -129,3 +138,25 @@ def test_bench_gemma_audio_reference_ops_match_oracle():
     got = bench.Gemma4AudioAttention.reference_ops(w, q, k, v, rel)
     ref = og.local_attention(q, k, v, rel, w.mask, 12, 12, 0, 50.0, -1e9)
     assert torch.equal(got, ref)
+
+
+def test_paged_layer_write_skips_rows_without_pages():
+    """A bucket's free row (block table -1) must not write into a page another
+    row owns: with the last pool page assigned to row 0, the unfused step's
+    cache write for rows [0, 1] leaves row 0's keys intact (qwen3_asr.py
+    ``PagedLayer.__setitem__``; torch indexing would map -1 to the last page)."""
+    from asrback_amd.qwen3_asr import PagedKVCache
+
+    config = {"num_hidden_layers": 1, "num_key_value_heads": 2, "head_dim": 8}
+    cache = PagedKVCache.allocate(config, batch=2, num_pages=3, page_size=16, device="cpu", dtype=torch.float32)
+    # Hand out pages until row 0 holds the last real page (2).
+    cache.assign(0, 16 * 3)
+    assert cache.block_table[0, :3].tolist() == [0, 1, 2]
+    layer = cache.keys[0]
+    rows = torch.tensor([0, 1])
+    positions = torch.tensor([32, 0])  # row 0: page 2, slot 0; row 1: no page
+    value = torch.stack([torch.full((2, 8), 7.0), torch.full((2, 8), -5.0)])
+    layer[rows, positions] = value
+    assert torch.equal(cache.pool_keys[0, 2, 0], torch.full((2, 8), 7.0))
+    assert not (cache.pool_keys[0, :3] == -5.0).any()  # the free row's write went to the sink page
+
