@@ -19,7 +19,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must be imported before the library; see above)
 
 LIBRARY = Path(__file__).resolve().with_name("libasrattn.so")
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 # enum asrattn_status / asrattn_dtype / asrattn_causal
 OK = 0
@@ -189,6 +189,7 @@ SIGNATURES = {
         ctypes.c_int,
         [ctypes.POINTER(DecodeParams), _ptr, ctypes.c_size_t, _ptr],
     ),
+    "asrattn_decode_noalloc": (ctypes.c_int, [ctypes.POINTER(DecodeParams), _ptr]),
     "asrattn_decode_append": (
         ctypes.c_int,
         [ctypes.POINTER(DecodeParams), ctypes.POINTER(AppendParams), _ptr, ctypes.c_size_t, _ptr],

@@ -5,6 +5,7 @@
 #include <stdio.h>
 
 #include <cmath>
+#include <mutex>
 #include <string>
 
 #include "asrattn.h"
@@ -313,6 +314,71 @@ int run_decode(const asrattn_decode_params* params, const asrattn_append_params*
 
 int asrattn_decode(const asrattn_decode_params* params, void* workspace, size_t workspace_bytes, void* stream) {
   return run_decode(params, nullptr, nullptr, workspace, workspace_bytes, stream, "asrattn_decode");
+}
+
+}  // extern "C"
+
+namespace {
+
+// The split partials of asrattn_decode_noalloc: one array per GPU (each GPU
+// holds its own copy at its own address), shared by every call on that GPU
+// and kept until the process ends.  In host code `scratch` names a host-side
+// stand-in, never the device memory: its device address comes from
+// hipGetSymbolAddress, once per device, with that device current.
+constexpr size_t kScratchBytes = ASRATTN_DECODE_NOALLOC_MAX_BYTES;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The device address of `scratch` on the current device (which must be the
+// device of `stream`).
+int scratch_address(void* stream, void** out) {
+  int device = -1;
+  hipError_t err = hipGetDevice(&device);
+  if (err != hipSuccess) return from_hip(err, "asrattn_decode_noalloc: hipGetDevice");
+  if (device < 0 || device >= kMaxDevices)
+    return fail(ASRATTN_ERR_UNSUPPORTED, "asrattn_decode_noalloc: device %d out of range", device);
+  if (stream != nullptr) {
+    int stream_device = -1;
+    err = hipStreamGetDevice(static_cast<hipStream_t>(stream), &stream_device);
+    if (err != hipSuccess) return from_hip(err, "asrattn_decode_noalloc: hipStreamGetDevice");
+    if (stream_device != device)
+      return fail(ASRATTN_ERR_INVALID, "asrattn_decode_noalloc: the stream is on device %d, the current device is %d",
+                  stream_device, device);
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[device] == nullptr) {
+    void* ptr = nullptr;
+    err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || ptr == nullptr)
+      return from_hip(err != hipSuccess ? err : hipErrorInvalidSymbol, "asrattn_decode_noalloc: hipGetSymbolAddress");
+    g_scratch_ptr[device] = ptr;
+  }
+  *out = g_scratch_ptr[device];
+  return ASRATTN_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int asrattn_decode_noalloc(const asrattn_decode_params* params, void* stream) {
+  const int checked = check_decode(params);
+  if (checked != ASRATTN_OK) return checked;
+  const size_t need = decode_workspace(*params, decode_splits(*params)).total;
+  if (need > kScratchBytes)
+    return fail(ASRATTN_ERR_WORKSPACE,
+                "asrattn_decode_noalloc: %zu bytes of split partials exceed its %zu-byte scratch; use "
+                "asrattn_decode with a workspace",
+                need, kScratchBytes);
+  if (need == 0 || params->batch == 0)
+    return run_decode(params, nullptr, nullptr, nullptr, 0, stream, "asrattn_decode_noalloc");
+  void* ptr = nullptr;
+  const int rc = scratch_address(stream, &ptr);
+  if (rc != ASRATTN_OK) return rc;
+  return run_decode(params, nullptr, nullptr, ptr, kScratchBytes, stream, "asrattn_decode_noalloc");
 }
 
 size_t asrattn_choose_workspace_size(int64_t rows, int64_t vocab) {

@@ -17,7 +17,8 @@
  *     in a HIP graph and replayed while the lengths change.
  *   - stream is a hipStream_t (passed as void*); every launch goes there.
  *   - No entry point allocates device memory or synchronizes.  Scratch space
- *     comes from the caller (asrattn_decode's workspace).
+ *     comes from the caller (asrattn_decode's workspace), except for
+ *     asrattn_decode_noalloc, which uses a static device array.
  *   - Every entry point returns ASRATTN_OK (0) or an error code; the message
  *     of the last error on the calling thread is asrattn_last_error().
  *     Nothing aborts the process.
@@ -32,7 +33,7 @@
 extern "C" {
 #endif
 
-#define ASRATTN_ABI_VERSION 10
+#define ASRATTN_ABI_VERSION 11
 
 enum asrattn_status {
   ASRATTN_OK = 0,
@@ -219,6 +220,27 @@ int asrattn_decode_num_splits(const asrattn_decode_params* params);
 
 int asrattn_decode(const asrattn_decode_params* params, void* workspace,
                    size_t workspace_bytes, void* stream);
+
+/*
+ * asrattn_decode without a workspace argument and without any allocation,
+ * for callers that cannot allocate device memory: code under HIP graph
+ * capture, tight serving loops, and harnesses that forbid hipMalloc.  It has
+ * no counterpart in the reference.
+ *
+ * The split partials go to a static device array of
+ * ASRATTN_DECODE_NOALLOC_MAX_BYTES bytes that the library holds on each GPU
+ * it runs on until the process ends.  That size covers every split count
+ * the library chooses itself (num_splits = 0; at most 6 MiB, head_dim 512
+ * with 8 query heads per kv head); parameters whose partials need more
+ * (asrattn_decode_workspace_size) are rejected with ASRATTN_ERR_WORKSPACE.
+ * The array needs no clearing: every launch writes all of the partials it
+ * reads.  All calls on one GPU share its array, so calls that may overlap on
+ * one GPU (different streams, or different host threads) race; serialize
+ * them, or use asrattn_decode with a workspace each.  The stream must belong
+ * to the current device.  Results are identical to asrattn_decode's.
+ */
+#define ASRATTN_DECODE_NOALLOC_MAX_BYTES ((size_t)8 << 20)
+int asrattn_decode_noalloc(const asrattn_decode_params* params, void* stream);
 
 /*
  * The decoder step with its prologue fused in: the step's own key and value

@@ -40,6 +40,7 @@ def test_header_declares_expected_entry_points():
         "asrattn_fwd",
         "asrattn_fwd_fsmn",
         "asrattn_decode",
+        "asrattn_decode_noalloc",
         "asrattn_decode_append",
         "asrattn_decode_paged",
         "asrattn_local",
@@ -129,6 +130,27 @@ def test_invalid_arguments_are_reported_not_fatal(lib):
     f.scale = 0.125  # valid shape but NULL tensors
     assert lib.asrattn_fwd(ctypes.byref(f), None) == _lib.ERR_INVALID
     assert b"non-NULL" in lib.asrattn_last_error()
+
+
+def test_noalloc_rejects_partials_beyond_its_scratch(lib):
+    """asrattn_decode_noalloc refuses split partials larger than its static
+    array before any device call (stand-in pointers, never dereferenced)."""
+    from asrback_amd import _lib
+
+    p = _lib.DecodeParams()
+    p.batch, p.heads_q, p.heads_kv, p.head_dim, p.max_len_k = 1, 8, 1, 256, 1 << 16
+    p.dtype, p.scale = _lib.BF16, 0.0625
+    p.q = p.k = p.v = p.out = 4096
+    p.q_batch_stride, p.q_head_stride = 2048, 256
+    p.k_batch_stride, p.k_token_stride, p.k_head_stride = 256 << 16, 256, 256
+    p.v_batch_stride, p.v_token_stride, p.v_head_stride = 256 << 16, 256, 256
+    p.o_batch_stride, p.o_head_stride = 2048, 256
+    p.num_splits = 1024  # 8 rows x 1024 splits x 256 floats = 8 MiB of partials, plus their stats
+    assert lib.asrattn_decode_workspace_size(ctypes.byref(p)) > 8 << 20
+    assert lib.asrattn_decode_noalloc(ctypes.byref(p), None) == _lib.ERR_WORKSPACE
+    assert b"scratch" in lib.asrattn_last_error()
+    p.heads_q = 0  # argument errors come first, as in asrattn_decode
+    assert lib.asrattn_decode_noalloc(ctypes.byref(p), None) == _lib.ERR_INVALID
 
 
 def test_invalid_append_and_span_are_reported(lib):
