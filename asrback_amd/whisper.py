@@ -171,7 +171,12 @@ class DecoderCache:
 
 
 class DecoderLayer(nn.Module):
-    """``whisper.py:199-241``."""
+    """``whisper.py:199-241``.  ``fused_step`` (on by default): the graphed
+    step writes the new key and value in its attention launch; off, it runs
+    the reference's two ``scatter_`` writes before the attention (the same
+    results; kept for comparisons)."""
+
+    fused_step = True
 
     def __init__(self, config: dict) -> None:
         super().__init__()
@@ -196,7 +201,7 @@ class DecoderLayer(nn.Module):
         self_keys, self_values, cross_keys, cross_values = cache
         hidden = self.self_attn_layer_norm(x)
         key, value = self.self_attn.project_key_value(hidden)
-        if length is None and isinstance(mask, KeyPrefix) and mask.positions is positions:
+        if self.fused_step and length is None and isinstance(mask, KeyPrefix) and mask.positions is positions:
             # The graphed step (one token per row, rows at different
             # positions, each seeing keys up to its own): cache write and
             # attention in one launch.

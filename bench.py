@@ -6,8 +6,11 @@ encoder self-attention in bf16 (4 heads x 128, 70 layers, batch 32 with
 ragged lengths of 104-504 frames and key padding): a step is the attention of
 all 70 layers over one batch, q/k/v read in place from per-layer fused
 projection buffers (token stride 1536) already resident in HBM, the 70
-launches replayed from one hipGraph.  ``value`` is algorithmic TFLOP/s:
-sum_b 4 * L_b^2 * 512 per layer over valid queries x valid keys.
+launches replayed from one hipGraph.  As ``SANMAttention`` runs it, padded
+query rows (t >= L_b) are not computed and get zeros.  ``value`` is
+algorithmic TFLOP/s: sum_b 4 * L_b^2 * 512 per layer over valid queries x
+valid keys.  Every figure is the median over the timed steps, each step
+bracketed by HIP events on the stream the graph replays on.
 
 Decode is reported beside it (``decode``): Qwen3-ASR-1.7B's GQA decoder step
 (28 layers, 16 query / 8 kv heads x 128, batch 64, prompts of 400-430 tokens,
@@ -25,20 +28,35 @@ the same launch (timed beside the reference's ops for both outputs), Whisper
 large-v3-turbo's encoder attention (20 heads x 64, 1500 frames, batch 16, 32
 layers), Qwen3's causal grouped-query prompt pass and its audio encoder's
 windowed attention, Gemma 4's blocked local audio attention and Gemma 4's
-windowed prompt pass.
+windowed prompt pass.  ``whisper_tiny`` holds Whisper-tiny's float32 lines
+(encoder attention against the fp32 matrix peak, the greedy decoder step's
+attention), ``whole_step`` Whisper-small's whole greedy decoder step with
+the cache write fused into the attention launch against the reference's
+separate writes.
 
 ``cpu_baseline`` times the CPU restatement of the reference's attention
-(torch SDPA with the key-padding mask, float32, the reference's CPU path) on
-a bounded sample of the headline workload on this machine's host cores.
+(torch SDPA with the reference's masks, float32, the reference's CPU path)
+on a bounded sample of the same workload on this machine's host cores: the
+headline and each of the other configurations' lines carry one.
+
+``roofline.traffic`` is the HBM bytes per launch of the dominant kernel from
+the FETCH_SIZE / WRITE_SIZE counter runs that ``--profile`` records in
+profiles/hbm_traffic.md, used only while the kernel sources still hash to
+what that run measured (else null, with a note).
 
     python bench.py [--steps K] [--warmup W] [--no-cpu-baseline] [--only NAME]
+    python bench.py --profile DIR [--only NAME]   (rocprofv3 runs; no GPU use in this process)
 """
 
 from __future__ import annotations
 
 import argparse
+import ctypes
+import hashlib
 import json
 import os
+import statistics
+import subprocess
 import sys
 import time
 from pathlib import Path
@@ -49,7 +67,9 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAK_FP32_TFLOPS = 157.3  # MI355X dense fp32 matrix
 PEAK_HBM_GBS = 8000.0  # MI355X HBM3E
+TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic.md"
 METRIC = "attn TFLOP/s (encoder) & HBM GB/s (decode step), % of MI355X roofline"
 
 
@@ -66,6 +86,8 @@ class Workload:
     kernel: str  # the dominant kernel (rocprof name prefix)
     launches: int  # launches of ``kernel`` per step
     work_per_step: float  # flop or bytes
+    peak: float = 0.0  # the roofline's peak; 0: bf16 MFMA for TFLOP/s, HBM for GB/s
+    dtype: str = "bf16"
 
     def run(self) -> None:
         raise NotImplementedError
@@ -110,7 +132,7 @@ class SenseVoiceEncoder(Workload):
     def run(self) -> None:
         for layer in range(self.layers):
             q, k, v = self.views(layer)
-            self.attention.flash(q, k, v, seqused_k=self.lengths, out=self.out)
+            self.attention.flash(q, k, v, seqused_k=self.lengths, out=self.out, zero_padded_rows=True)
 
     def config(self) -> dict:
         return {
@@ -122,6 +144,7 @@ class SenseVoiceEncoder(Workload):
             "frames": "U{100..500} + 4 queries, key padding",
             "lengths_mean": float(self.lengths_host.mean()),
             "max_length": self.length,
+            "padded_rows": "zeros (not computed), as SANMAttention runs it",
         }
 
 
@@ -161,7 +184,7 @@ class SenseVoiceAttentionFsmn(SenseVoiceEncoder):
             if self.mode in ("fused", "module"):
                 self.attention.flash_fsmn(q, k, v, self.weight[layer], seqused_k=self.lengths,
                                           bias=self.bias[layer] if module else None, out=self.out,
-                                          memory=self.memory)
+                                          memory=self.memory, zero_padded_rows=True)
                 if module:
                     self.memory.view(-1, width).addmm_(self.out.view(-1, width), self.w_out[layer].t())
                 continue
@@ -169,7 +192,7 @@ class SenseVoiceAttentionFsmn(SenseVoiceEncoder):
             memory = F.pad(masked.transpose(1, 2), (5, 5))
             memory = F.conv1d(memory, self.weight[layer], groups=width).transpose(1, 2) + masked
             memory = memory * self.keep
-            self.attention.flash(q, k, v, seqused_k=self.lengths, out=self.out)
+            self.attention.flash(q, k, v, seqused_k=self.lengths, out=self.out, zero_padded_rows=True)
             if module:
                 memory = F.linear(self.out.view(self.batch, self.length, width), self.w_out[layer],
                                   self.bias[layer]) + memory
@@ -738,6 +761,157 @@ class WhisperSmallDecoderStep(Workload):
                 "layers": self.layers, "self_keys": "U{1..224} in a 256 bucket", "cross_frames": 1500}
 
 
+WHISPER_TINY = {"d_model": 384, "heads": 6, "layers": 4, "frames": 1500, "prefix": 4, "steps": 32}
+
+
+class WhisperTinyEncoder(Workload):
+    """Whisper-tiny's encoder self-attention in float32 (whisper.py:102-110):
+    one 30 s window, 6 heads x 64 over 1500 frames, 4 layers, q/k/v views of
+    per-layer ``(1, 1500, 1152)`` projections.  Value: TFLOP/s of ``4 * 1500^2
+    * 384`` per layer against the fp32 matrix peak."""
+
+    name = "whisper-tiny-encoder-attention-fp32"
+    unit = "TFLOP/s"
+    bound = "mfma"
+    kernel = "fwd_"
+    peak = PEAK_FP32_TFLOPS
+    dtype = "f32"
+
+    def __init__(self, torch, attention, seed: int = 9) -> None:
+        self.width, self.heads, self.layers, self.length = (WHISPER_TINY[k] for k in ("d_model", "heads", "layers",
+                                                                                      "frames"))
+        g = torch.Generator(device="cuda").manual_seed(seed)
+        self.qkv = [torch.randn((1, self.length, 3 * self.width), generator=g, device="cuda")
+                    for _ in range(self.layers)]
+        self.out = torch.empty((1, self.length, self.heads, self.width // self.heads), device="cuda")
+        self.attention = attention
+        self.launches = self.layers
+        self.work_per_step = 4.0 * self.length**2 * self.width * self.layers
+
+    def run(self) -> None:
+        shape = (1, self.length, self.heads, self.width // self.heads)
+        for layer in range(self.layers):
+            q, k, v = (t.view(shape) for t in self.qkv[layer].split(self.width, dim=-1))
+            self.attention.flash(q, k, v, out=self.out)
+
+    def config(self) -> dict:
+        return {"workload": self.name, "batch": 1, "heads": self.heads, "head_dim": self.width // self.heads,
+                "layers": self.layers, "frames": self.length, "dtype": "float32"}
+
+
+class WhisperTinyDecodeStep(Workload):
+    """Whisper-tiny's greedy decoder step in float32 (whisper.py:212-277),
+    one row: per layer, self-attention over keys 0..position of the ``(1, 6,
+    448, 64)`` cache (the 4-token prompt, then 32 steps: positions 4..35) and
+    cross-attention over the 1500 encoder frames.  Value: algorithmic HBM
+    GB/s (K and V of the keys each launch uses, plus q and o)."""
+
+    name = "whisper-tiny-decoder-step-attention-fp32"
+    unit = "GB/s"
+    bound = "hbm"
+    kernel = "decode_kernel"
+    dtype = "f32"
+
+    def __init__(self, torch, attention, seed: int = 10) -> None:
+        self.width, self.heads, self.layers = WHISPER_TINY["d_model"], WHISPER_TINY["heads"], WHISPER_TINY["layers"]
+        self.steps = WHISPER_TINY["steps"]
+        hd = self.width // self.heads
+        g = torch.Generator(device="cuda").manual_seed(seed)
+        self.self_kv = torch.randn((2, self.layers, 1, self.heads, 448, hd), generator=g, device="cuda")
+        self.cross_kv = torch.randn((2, self.layers, 1, self.heads, 1500, hd), generator=g, device="cuda")
+        self.q = torch.randn((self.layers, 2, 1, self.heads, hd), generator=g, device="cuda")
+        self.out = torch.empty((1, self.heads, hd), device="cuda")
+        self.start = torch.full((1,), WHISPER_TINY["prefix"] - 1, dtype=torch.int64, device="cuda")
+        self.positions = self.start.clone()
+        self.attention = attention
+        self.launches = 2 * self.layers
+        row = self.width * 4
+        self.step_bytes = [
+            float(self.layers * (2 * row * (WHISPER_TINY["prefix"] + t + 1) + 2 * row * 1500 + 4 * row))
+            for t in range(self.steps)
+        ]
+        self.work_per_step = float(np.mean(self.step_bytes))
+
+    def reset(self) -> None:
+        self.positions.copy_(self.start)
+
+    def run(self) -> None:
+        self.positions.add_(1)
+        for layer in range(self.layers):
+            keys, values = (t[layer, :, :, :64].transpose(1, 2) for t in self.self_kv)
+            self.attention.decode(self.q[layer, 0], keys, values, positions=self.positions, out=self.out)
+            keys, values = (t[layer].transpose(1, 2) for t in self.cross_kv)
+            self.attention.decode(self.q[layer, 1], keys, values, out=self.out)
+
+    def config(self) -> dict:
+        return {"workload": self.name, "batch": 1, "heads": self.heads, "head_dim": self.width // self.heads,
+                "layers": self.layers, "self_keys": "5..36 in a 64 bucket (4-token prompt, 32 steps)",
+                "cross_frames": 1500, "steps": self.steps, "dtype": "float32"}
+
+
+class WhisperSmallWholeStep(Workload):
+    """Whisper-small's whole greedy decoder step (whisper.py:942-960: token and
+    position embeddings, 12 decoder layers, the logits, the greedy choice and
+    the state update) in bf16 with random-init weights: 16 rows at positions
+    U{0..223} over the 256-position KV bucket, cross-attention over 1500
+    frames, one hipGraph per form.  With ``DecoderLayer.fused_step`` each
+    layer's new key and value are written by its attention launch
+    (``decode_append``); without it, by the reference's two ``scatter_``
+    writes before the attention launch.  Value: decoder steps per second of
+    the fused form; ``kernels_per_step`` counts the graph's kernel nodes."""
+
+    name = "whisper-small-decoder-whole-step"
+    unit = "steps/s"
+    bound = "hbm"
+    kernel = "decode_kernel"
+
+    def __init__(self, torch, attention, seed: int = 4, steps: int = 32) -> None:
+        from asrback_amd import whisper as aw
+
+        self.torch, self.aw, self.steps = torch, aw, steps
+        config = {"d_model": 768, "encoder_attention_heads": 12, "decoder_attention_heads": 12,
+                  "encoder_layers": 12, "decoder_layers": 12, "encoder_ffn_dim": 3072, "decoder_ffn_dim": 3072,
+                  "num_mel_bins": 80, "max_source_positions": 1500, "max_target_positions": 448,
+                  "vocab_size": 51865, "eos_token_id": 50257}
+        torch.manual_seed(seed)
+        with torch.device("cuda"):
+            model = aw.WhisperForConditionalGeneration(config)
+        model = model.to(torch.bfloat16).eval().requires_grad_(False)
+        vocab = config["vocab_size"]
+        suppress = torch.zeros(vocab, dtype=torch.bool)
+        suppress[50257:] = True  # special tokens, as the reference's suppress list holds them
+        self.batch = 16
+        self.decoder = aw.GreedyDecoder(model, self.batch, suppress, suppress, config["eos_token_id"], graphs=False)
+        cache = self.decoder.cache
+        g = torch.Generator(device="cuda").manual_seed(seed)
+        for tensor in (cache.self_keys, cache.self_values, cache.cross_keys, cache.cross_values):
+            tensor.copy_(torch.randn(tensor.shape, generator=g, device="cuda", dtype=torch.bfloat16))
+        rng = np.random.default_rng(seed)
+        self.start = torch.from_numpy(rng.integers(0, 224, size=self.batch).astype(np.int64)).cuda()
+        self.tokens = torch.from_numpy(rng.integers(0, 50257, size=(self.batch, 1)).astype(np.int64)).cuda()
+        self.state = self.decoder.state.narrow(self.batch)
+        self.view = cache.narrow(self.batch, 256)
+        self.state.end.fill_(255)
+        self.reset()
+        self.attention = attention
+        self.launches = 2 * config["decoder_layers"]
+        self.work_per_step = 1.0  # one step
+
+    def reset(self) -> None:
+        self.state.position.copy_(self.start)
+        self.state.tokens.copy_(self.tokens)
+        self.state.finished.zero_()
+
+    def run(self) -> None:
+        with self.torch.no_grad():
+            self.decoder.step(self.state, self.view)
+
+    def config(self) -> dict:
+        return {"workload": self.name, "model": "whisper-small decoder (random init)", "batch": self.batch,
+                "heads": 12, "head_dim": 64, "layers": 12, "self_keys": "U{1..224} in a 256 bucket",
+                "cross_frames": 1500}
+
+
 class CopyCalibration(Workload):
     """A plain device-to-device copy of 1 GiB: the known-size kernel that
     scales the HBM traffic counters (FETCH_SIZE / WRITE_SIZE)."""
@@ -761,10 +935,47 @@ class CopyCalibration(Workload):
         return {"workload": self.name, "bytes_read": 1 << 30, "bytes_written": 1 << 30}
 
 
-def time_graph(torch, workload: Workload, steps: int, warmup: int, reset=None) -> float:
-    """Milliseconds per step: the step captured once as a hipGraph, ``warmup``
-    untimed replays, then ``steps`` replays between HIP events on the
-    launching stream, with a device synchronization on both sides."""
+_hip = None
+
+
+def hip_runtime():
+    """The HIP runtime torch loaded (the same library handle, found by path)."""
+    global _hip
+    if _hip is None:
+        for line in open("/proc/self/maps"):
+            if "libamdhip64" in line:
+                _hip = ctypes.CDLL(line.split()[-1])
+                break
+    return _hip
+
+
+def kernel_nodes(graph) -> int | None:
+    """Kernel nodes of a captured graph (hipGraphGetNodes / hipGraphNodeGetType)."""
+    hip = hip_runtime()
+    if hip is None:
+        return None
+    handle = ctypes.c_void_p(graph.raw_cuda_graph())
+    count = ctypes.c_size_t(0)
+    if hip.hipGraphGetNodes(handle, None, ctypes.byref(count)) != 0:
+        return None
+    nodes = (ctypes.c_void_p * count.value)()
+    if hip.hipGraphGetNodes(handle, nodes, ctypes.byref(count)) != 0:
+        return None
+    kernels = 0
+    kind = ctypes.c_int(-1)
+    for node in nodes:
+        if hip.hipGraphNodeGetType(ctypes.c_void_p(node), ctypes.byref(kind)) != 0:
+            return None
+        kernels += kind.value == 0  # hipGraphNodeTypeKernel
+    return kernels
+
+
+def time_graph(torch, workload: Workload, steps: int, warmup: int) -> dict:
+    """The step captured once as a hipGraph, ``warmup`` untimed replays, then
+    ``steps`` replays, each between HIP events on the replaying stream, with
+    a device synchronization on both sides.  Returns the median and mean
+    milliseconds per step and the graph's kernel nodes."""
+    reset = getattr(workload, "reset", None)
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(stream):
@@ -772,9 +983,11 @@ def time_graph(torch, workload: Workload, steps: int, warmup: int, reset=None) -
             workload.run()
     torch.cuda.current_stream().wait_stream(stream)
     torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
+    graph = torch.cuda.CUDAGraph(keep_graph=True)
     with torch.cuda.graph(graph):
         workload.run()
+    graph.instantiate()
+    kernels = kernel_nodes(graph)
     if reset is not None:
         reset()
     for _ in range(warmup):
@@ -782,52 +995,59 @@ def time_graph(torch, workload: Workload, steps: int, warmup: int, reset=None) -
     if reset is not None:
         reset()
     torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    stop = torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(steps):
+    events = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    events[0].record()
+    for i in range(steps):
         graph.replay()
-    stop.record()
+        events[i + 1].record()
     torch.cuda.synchronize()
-    return start.elapsed_time(stop) / steps
+    per_step = [events[i].elapsed_time(events[i + 1]) for i in range(steps)]
+    return {"median": statistics.median(per_step), "mean": events[0].elapsed_time(events[-1]) / steps,
+            "kernels": kernels}
 
 
-def measured_traffic() -> dict:
-    """HBM bytes per launch of the dominant kernels, from the FETCH_SIZE /
-    WRITE_SIZE counter runs recorded in profiles/hbm_traffic.md (scaled by
-    the counters' reading for a 1 GiB copy)."""
-    path = ROOT / "profiles" / "hbm_traffic.md"
+def sources_digest() -> str:
+    """Hash of the kernel library's sources (csrc and the C header)."""
+    csrc = ROOT / "asrback_amd" / "csrc"
+    h = hashlib.sha256()
+    for path in sorted(list(csrc.glob("*.hip")) + list(csrc.glob("*.hpp"))) + [ROOT / "include" / "asrattn.h"]:
+        h.update(path.name.encode())
+        h.update(path.read_bytes())
+    return h.hexdigest()[:16]
+
+
+def read_traffic() -> dict:
+    """The JSON block of profiles/hbm_traffic.md ({} when absent)."""
     try:
-        text = path.read_text()
-        block = text.split("```json", 1)[1].split("```", 1)[0]
-        return json.loads(block)["workloads"]
-    except (OSError, IndexError, ValueError, KeyError):
+        text = TRAFFIC_FILE.read_text()
+        return json.loads(text.split("```json", 1)[1].split("```", 1)[0])
+    except (OSError, IndexError, ValueError):
         return {}
 
 
-TRAFFIC_KEYS = {
-    "sensevoice-small-encoder-attention": "sensevoice",
-    "qwen3-asr-1.7b-decode-attention": "qwen3",
-    "whisper-small-decoder-step-attention": "whisper-small",
-    "whisper-large-v3-turbo-encoder-attention": "turbo",
-    "qwen3-asr-1.7b-decode-attention-paged": "qwen3-paged",
-    "qwen3-asr-1.7b-prefill-attention": "qwen3-prefill",
-    "qwen3-asr-audio-encoder-attention": "qwen3-audio",
-    "gemma4-audio-local-attention": "gemma4-audio",
-    "gemma4-text-decode-attention": "gemma4-decode",
-    "gemma4-prefill-attention": "gemma4-prefill",
-}
+def measured_traffic(key: str) -> tuple[float | None, str | None]:
+    """HBM bytes per launch of ``key``'s dominant kernel from the counter
+    runs, or None and the reason."""
+    record = read_traffic()
+    if not record:
+        return None, "no counter run recorded"
+    if record.get("sources") != sources_digest():
+        return None, "the counter run measured other kernel sources"
+    entry = record.get("workloads", {}).get(key)
+    if not entry:
+        return None, "not in the counter run"
+    return entry["bytes_per_launch"], None
 
 
-def roofline(workload: Workload, ms_per_step: float, work_per_step: float) -> dict:
+def roofline(workload: Workload, key: str, ms_per_step: float, work_per_step: float) -> dict:
     seconds = ms_per_step / 1e3
     if workload.unit == "TFLOP/s":
         achieved = work_per_step / seconds / 1e12
-        peak = PEAK_BF16_TFLOPS
+        peak = workload.peak or PEAK_BF16_TFLOPS
     else:
         achieved = work_per_step / seconds / 1e9
-        peak = PEAK_HBM_GBS
-    traffic = measured_traffic().get(TRAFFIC_KEYS.get(workload.name, ""), {}).get("bytes_per_launch")
+        peak = workload.peak or PEAK_HBM_GBS
+    traffic, note = measured_traffic(key)
     line = {
         "bound": workload.bound,
         "achieved": round(achieved, 2),
@@ -839,6 +1059,8 @@ def roofline(workload: Workload, ms_per_step: float, work_per_step: float) -> di
         "launches_per_step": workload.launches,
         "avg_launch_us": round(ms_per_step * 1e3 / workload.launches, 2),
     }
+    if note:
+        line["traffic_note"] = note
     if workload.unit == "TFLOP/s" and traffic:
         # The attainable rate given the launch's measured HBM traffic: flops
         # per byte times the HBM peak, capped by the matrix-core peak.
@@ -850,101 +1072,239 @@ def roofline(workload: Workload, ms_per_step: float, work_per_step: float) -> di
     return line
 
 
-def measure(torch, workload: Workload, steps: int, warmup: int) -> dict:
-    if hasattr(workload, "step_bytes"):
-        # The 128-step decodes: the timed steps advance the positions.
+def timed_against(torch, workload: Workload, steps: int, warmup: int, result: dict, attr: str, value,
+                  prefix: str = "unfused") -> None:
+    """Time ``workload`` again with ``attr`` set to ``value`` and add it to
+    ``result`` as ``{prefix}_ms_per_step`` (and its kernel count)."""
+    owner = workload.aw.DecoderLayer if attr == "fused_step" else workload
+    saved = getattr(owner, attr)
+    setattr(owner, attr, value)
+    try:
+        other = time_graph(torch, workload, steps, warmup)
+    finally:
+        setattr(owner, attr, saved)
+    result[f"{prefix}_ms_per_step"] = round(other["median"], 4)
+    result[f"{prefix}_kernels_per_step"] = other["kernels"]
+    if prefix == "unfused":
+        result["speedup_vs_unfused"] = round(other["median"] / result["ms_per_step"], 3)
+
+
+def measure(torch, workload: Workload, key: str, steps: int, warmup: int, compare: bool = True) -> dict:
+    if hasattr(workload, "steps"):
+        # Workloads that advance positions: at most their step count is timed.
         steps = min(steps, workload.steps)
-        ms = time_graph(torch, workload, steps, min(warmup, workload.steps), reset=workload.reset)
-        work = float(np.mean(workload.step_bytes[:steps]))
+        warmup = min(warmup, workload.steps)
+    timing = time_graph(torch, workload, steps, warmup)
+    ms = timing["median"]
+    step_bytes = getattr(workload, "step_bytes", None)
+    work = float(np.mean(step_bytes[:steps])) if step_bytes else workload.work_per_step
+    if workload.unit == "steps/s":
+        value = 1e3 / ms
     else:
-        ms = time_graph(torch, workload, steps, warmup)
-        work = workload.work_per_step
-    seconds = ms / 1e3
-    value = work / seconds / (1e12 if workload.unit == "TFLOP/s" else 1e9)
+        value = work / (ms / 1e3) / (1e12 if workload.unit == "TFLOP/s" else 1e9)
     result = {
         "workload": workload.name,
         "value": round(value, 2),
         "unit": workload.unit,
+        "dtype": workload.dtype,
         "ms_per_step": round(ms, 4),
-        "roofline": roofline(workload, ms, work),
+        "ms_per_step_mean": round(timing["mean"], 4),
+        "steps_timed": steps,
+        "kernels_per_step": timing["kernels"],
+        "roofline": None if workload.unit == "steps/s" else roofline(workload, key, ms, work),
         "config": workload.config(),
+        "work_per_launch": work / workload.launches,
     }
-    if isinstance(workload, GreedyChoice):
-        workload.unfused = True
-        unfused = time_graph(torch, workload, steps, warmup)
-        workload.unfused = False
-        result["unfused_ms_per_step"] = round(unfused, 4)
-        result["speedup_vs_unfused"] = round(unfused / ms, 3)
+    if not compare:
+        return result
+    if isinstance(workload, (GreedyChoice, Gemma4AudioAttention, Qwen3DecodeStepFused)):
+        timed_against(torch, workload, steps, warmup, result, "unfused", True)
+    if isinstance(workload, WhisperSmallWholeStep):
+        timed_against(torch, workload, steps, warmup, result, "fused_step", False)
+        result["saved_kernels_per_step"] = (None if result["kernels_per_step"] is None
+                                            or result["unfused_kernels_per_step"] is None
+                                            else result["unfused_kernels_per_step"] - result["kernels_per_step"])
     if isinstance(workload, SenseVoiceAttentionFsmn):
-        timed = {}
         for mode in ("unfused", "module", "module_unfused"):
-            workload.mode = mode
-            timed[mode] = time_graph(torch, workload, steps, warmup)
-        workload.mode = "fused"
-        result["unfused_ms_per_step"] = round(timed["unfused"], 4)
-        result["speedup_vs_unfused"] = round(timed["unfused"] / ms, 3)
-        result["module_ms_per_step"] = round(timed["module"], 4)
-        result["module_unfused_ms_per_step"] = round(timed["module_unfused"], 4)
-        result["module_speedup_vs_unfused"] = round(timed["module_unfused"] / timed["module"], 3)
-    if isinstance(workload, Gemma4AudioAttention):
-        workload.unfused = True
-        unfused = time_graph(torch, workload, steps, warmup)
-        workload.unfused = False
-        result["unfused_ms_per_step"] = round(unfused, 4)
-        result["speedup_vs_unfused"] = round(unfused / ms, 3)
-    if isinstance(workload, Qwen3DecodeStepFused):
-        workload.unfused = True
-        unfused = time_graph(torch, workload, steps, min(warmup, workload.steps), reset=workload.reset)
-        workload.unfused = False
-        result["unfused_ms_per_step"] = round(unfused, 4)
-        result["speedup_vs_unfused"] = round(unfused / ms, 3)
+            timed_against(torch, workload, steps, warmup, result, "mode", mode, prefix=mode)
+        result.pop("unfused_kernels_per_step", None)
+        result["speedup_vs_unfused"] = round(result["unfused_ms_per_step"] / ms, 3)
+        result["module_speedup_vs_unfused"] = round(result["module_unfused_ms_per_step"] /
+                                                    result["module_ms_per_step"], 3)
     return result
 
 
-def cpu_baseline(budget_s: float = 10.0) -> dict:
-    """The reference's CPU path (oracle: torch SDPA with the key-padding mask,
-    float32) on the headline batch: layers of attention (each a pass over
-    the batch) until ``budget_s`` seconds have passed."""
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return ""
+
+
+def _cpu_timed(fn, work: float, scale: float, unit: str, sample: str, budget_s: float) -> dict:
+    """``fn`` once untimed, then repeatedly until ``budget_s`` seconds (at
+    least three runs); the rate is ``work`` over the median run time."""
+    import torch
+
+    fn()
+    times = []
+    start = time.perf_counter()
+    while len(times) < 3 or time.perf_counter() - start < budget_s:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    median = statistics.median(times)
+    return {
+        "value": round(work / median / scale, 4),
+        "unit": unit,
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"{sample}; median of {len(times)} runs ({median * 1e3:.1f} ms each); {_cpu_model()}",
+        "seconds": round(sum(times), 2),
+    }
+
+
+def cpu_sensevoice(budget_s: float) -> dict:
+    """SAN-M attention of one layer over the headline batch (oracle: torch
+    SDPA with the key-padding mask, sensevoice.py:128-133)."""
     import torch
 
     from oracle import attention as oa
 
-    cores = len(os.sched_getaffinity(0))
-    torch.set_num_threads(cores)
     rng = np.random.default_rng(1)
-    frames = rng.integers(100, 501, size=32)
-    lengths = torch.from_numpy((frames + 4).astype(np.int64))
+    lengths = torch.from_numpy((rng.integers(100, 501, size=32) + 4).astype(np.int64))
     length = int(lengths.max())
-    g = torch.Generator().manual_seed(1)
-    qkv = torch.randn((32, length, 3 * 512), generator=g)
+    qkv = torch.randn((32, length, 3 * 512), generator=torch.Generator().manual_seed(1))
     mask = oa.key_padding_mask(lengths, length)
-    per_layer = float(sum(4 * int(n) ** 2 * 512 for n in lengths))
-    oa.sensevoice_attention(qkv, 4, mask)  # warm-up
-    layers = 0
-    start = time.perf_counter()
-    while True:
-        oa.sensevoice_attention(qkv, 4, mask)
-        layers += 1
-        elapsed = time.perf_counter() - start
-        if elapsed > budget_s:
-            break
-    model = ""
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                model = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
-    return {
-        "value": round(per_layer * layers / elapsed / 1e12, 4),
-        "unit": "TFLOP/s",
-        "cores": torch.get_num_threads(),
-        "kind": "port",
-        "sample": f"{layers} layer passes over the headline batch (B=32, lengths {int(lengths.min())}-"
-        f"{length}), float32, torch CPU SDPA with key-padding mask; {model}",
-        "seconds": round(elapsed, 2),
-    }
+    work = float(sum(4 * int(n) ** 2 * 512 for n in lengths))
+    return _cpu_timed(lambda: oa.sensevoice_attention(qkv, 4, mask), work, 1e12, "TFLOP/s",
+                      f"one layer over the headline batch (B=32, lengths {int(lengths.min())}-{length}), float32",
+                      budget_s)
+
+
+def cpu_turbo(budget_s: float) -> dict:
+    """Whisper large-v3-turbo encoder attention of one layer (whisper.py:102-104)."""
+    import torch
+
+    from oracle import attention as oa
+
+    g = torch.Generator().manual_seed(2)
+    q, k, v = (torch.randn((16, 20, 1500, 64), generator=g) for _ in range(3))
+    return _cpu_timed(lambda: oa.sdpa(q, k, v), 4.0 * 1500**2 * 1280 * 16, 1e12, "TFLOP/s",
+                      "one layer (B=16, 20 heads x 64, 1500 frames), float32", budget_s)
+
+
+def cpu_whisper_tiny_encoder(budget_s: float) -> dict:
+    """Whisper-tiny's encoder attention, all 4 layers (whisper.py:102-104)."""
+    import torch
+
+    from oracle import attention as oa
+
+    g = torch.Generator().manual_seed(9)
+    layers = [[torch.randn((1, 6, 1500, 64), generator=g) for _ in range(3)] for _ in range(4)]
+    return _cpu_timed(lambda: [oa.sdpa(*qkv) for qkv in layers], 4.0 * 1500**2 * 384 * 4, 1e12, "TFLOP/s",
+                      "the 4 layers of one window (6 heads x 64, 1500 frames), float32", budget_s)
+
+
+def _decode_sample(batch, heads_q, heads_kv, head_dim, cache, keys_used, seed):
+    """Inputs of one decode launch on the CPU: q, keys/values ``(B, H, L, D)``
+    and the step mask for ``keys_used`` (None: every key)."""
+    import torch
+
+    from oracle import attention as oa
+
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn((batch, heads_q, 1, head_dim), generator=g)
+    k, v = (torch.randn((batch, heads_kv, cache, head_dim), generator=g) for _ in range(2))
+    mask = None
+    if keys_used is not None:
+        mask = oa.whisper_step_mask(torch.as_tensor(keys_used, dtype=torch.int64) - 1, cache)
+    return q, k, v, mask
+
+
+def cpu_whisper_small(budget_s: float) -> dict:
+    """Whisper-small decoder step attention of one layer: self-attention with
+    the step mask over the 256 bucket (whisper.py:235-237) and
+    cross-attention over 1500 frames (:239-240)."""
+    from oracle import attention as oa
+
+    rng = np.random.default_rng(4)
+    used = rng.integers(0, 224, size=16) + 1
+    self_in = _decode_sample(16, 12, 12, 64, 256, used, 4)
+    cross_in = _decode_sample(16, 12, 12, 64, 1500, None, 5)
+    row = 12 * 64 * 2
+    work = float(sum(2 * row * int(n) + 2 * row for n in used) + 16 * (2 * row * 1500 + 2 * row))
+
+    def layer():
+        oa.sdpa(*self_in[:3], attn_mask=self_in[3])
+        oa.sdpa(*cross_in[:3])
+
+    return _cpu_timed(layer, work, 1e9, "GB/s",
+                      "one layer (B=16, self keys U{1..224} in a 256 bucket, cross 1500), float32; bytes "
+                      "counted as the bf16 workload's", budget_s)
+
+
+def cpu_whisper_tiny_step(budget_s: float) -> dict:
+    """Whisper-tiny decoder step attention, all 4 layers, at the 32-step
+    decode's middle position (keys 0..19 of a 64 bucket; cross 1500)."""
+    from oracle import attention as oa
+
+    layers = [(_decode_sample(1, 6, 6, 64, 64, [20], 10 + i), _decode_sample(1, 6, 6, 64, 1500, None, 20 + i))
+              for i in range(4)]
+    row = 384 * 4
+    work = float(4 * (2 * row * 20 + 2 * row * 1500 + 4 * row))
+
+    def step():
+        for self_in, cross_in in layers:
+            oa.sdpa(*self_in[:3], attn_mask=self_in[3])
+            oa.sdpa(*cross_in[:3])
+
+    return _cpu_timed(step, work, 1e9, "GB/s", "the 4 layers of one step (20 self keys, cross 1500), float32",
+                      budget_s)
+
+
+def cpu_qwen3_decode(budget_s: float) -> dict:
+    """Qwen3-ASR GQA decode of one layer at the 128-step decode's middle
+    step (qwen3_asr.py:427-432 on the padded path: query heads grouped per kv
+    head, the step mask over the 1024-position cache)."""
+    import torch
+
+    from oracle import attention as oa
+
+    rng = np.random.default_rng(3)
+    used = (390 + rng.integers(10, 41, size=64)) + 64
+    g = torch.Generator().manual_seed(3)
+    q = torch.randn((64, 16, 128), generator=g)
+    keys, values = (torch.randn((64, 1024, 8, 128), generator=g) for _ in range(2))
+    mask = oa.qwen_step_mask(torch.from_numpy(used - 1), 1024)
+    row = 2 * 8 * 128 * 2
+    work = float(sum(row * int(n) + 2 * 16 * 128 * 2 for n in used))
+    return _cpu_timed(lambda: oa.qwen_step_attention(q, keys, values, mask), work, 1e9, "GB/s",
+                      "one layer at step 64 (B=64, 16q/8kv x 128, 1024-position cache), float32; bytes counted "
+                      "as the bf16 workload's", budget_s)
+
+
+# Workloads (by --only key) that carry a CPU baseline: the headline and one
+# line per other configuration.
+CPU_BASELINES = {
+    "sensevoice": cpu_sensevoice,
+    "turbo": cpu_turbo,
+    "whisper-small": cpu_whisper_small,
+    "qwen3": cpu_qwen3_decode,
+    "whisper-tiny-encoder": cpu_whisper_tiny_encoder,
+    "whisper-tiny-step": cpu_whisper_tiny_step,
+}
+
+
+def cpu_baseline(key: str, budget_s: float) -> dict:
+    import torch
+
+    torch.set_num_threads(len(os.sched_getaffinity(0)))
+    with torch.inference_mode():
+        return CPU_BASELINES[key](budget_s)
 
 
 def shape_sweep(torch, attention) -> None:
@@ -995,17 +1355,251 @@ def shape_sweep(torch, attention) -> None:
         print(f"| {name} | {us:.2f} | {flops / us / 1e6:.1f} |", flush=True)
 
 
+WORKLOADS = {
+    "sensevoice": SenseVoiceEncoder,
+    "sensevoice-fsmn": SenseVoiceAttentionFsmn,
+    "turbo": WhisperTurboEncoder,
+    "qwen3": Qwen3Decode,
+    "qwen3-paged": Qwen3DecodePaged,
+    "qwen3-fused": Qwen3DecodeStepFused,
+    "qwen3-prefill": Qwen3Prefill,
+    "qwen3-audio": Qwen3AudioAttention,
+    "gemma4-audio": Gemma4AudioAttention,
+    "gemma4-decode": Gemma4TextDecode,
+    "gemma4-prefill": Gemma4Prefill,
+    "choice": GreedyChoice,
+    "whisper-small": WhisperSmallDecoderStep,
+    "whisper-tiny-encoder": WhisperTinyEncoder,
+    "whisper-tiny-step": WhisperTinyDecodeStep,
+    "whisper-small-step": WhisperSmallWholeStep,
+    "copy": CopyCalibration,
+}
+# The lines of the default run after the headline, by group.
+GROUPS = {
+    "decode": ["qwen3", "qwen3-paged", "qwen3-fused", "whisper-small", "choice", "gemma4-decode"],
+    "secondary": ["sensevoice-fsmn", "turbo", "qwen3-prefill", "qwen3-audio", "gemma4-audio", "gemma4-prefill"],
+    "whisper_tiny": ["whisper-tiny-encoder", "whisper-tiny-step"],
+    "whole_step": ["whisper-small-step"],
+}
+
+
+def _run_child(cmd: list[str], limit: float) -> tuple[int, str, str]:
+    """Run ``cmd`` in its own process group; kill the group at ``limit`` s."""
+    proc = subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True, start_new_session=True)
+    try:
+        out, err = proc.communicate(timeout=limit)
+    except subprocess.TimeoutExpired:
+        os.killpg(proc.pid, 9)
+        out, err = proc.communicate()
+        return 124, out, err
+    return proc.returncode, out, err
+
+
+def _result_line(stdout: str) -> dict | None:
+    for line in reversed(stdout.splitlines()):
+        if line.startswith("{"):
+            return json.loads(line)
+    return None
+
+
+def _csv_rows(directory: Path, suffix: str) -> list[dict]:
+    import csv
+
+    rows = []
+    for path in sorted(directory.rglob(f"*{suffix}")):
+        with open(path, newline="") as f:
+            rows.extend(csv.DictReader(f))
+    return rows
+
+
+def _dispatch_counters(directory: Path, counter: str) -> list[tuple[int, str, float]]:
+    """(dispatch id, kernel, value) of ``counter`` per dispatch, in dispatch order."""
+    values: dict[int, list] = {}
+    for row in _csv_rows(directory, "counter_collection.csv"):
+        if row.get("Counter_Name") != counter:
+            continue
+        dispatch = int(row["Dispatch_Id"])
+        entry = values.setdefault(dispatch, [row["Kernel_Name"], 0.0])
+        entry[1] += float(row["Counter_Value"])
+    return [(d, k, v) for d, (k, v) in sorted(values.items())]
+
+
+def profile(out: Path, keys: list[str], steps: int, warmup: int) -> int:
+    """rocprofv3 runs of each workload in child processes (this process
+    never touches the GPU): a plain run, a kernel trace, and one counter pass
+    each for FETCH_SIZE and WRITE_SIZE (plus the 1 GiB copy that scales
+    them).  Writes a summary per workload and hbm_traffic.md to
+    ``out/profiles``."""
+    out = out.resolve()
+    summaries = out / "profiles"
+    summaries.mkdir(parents=True, exist_ok=True)
+    digest = sources_digest()
+    bench = [sys.executable, "-u", str(ROOT / "bench.py")]
+
+    def child(key: str, tag: str, prof: list[str], n_steps: int, n_warmup: int) -> tuple[dict, Path, str]:
+        directory = out / key / tag
+        directory.mkdir(parents=True, exist_ok=True)
+        args = ["--only", key, "--steps", str(n_steps), "--warmup", str(n_warmup), "--no-cpu-baseline",
+                "--no-compare"]
+        cmd = bench + args
+        if prof:
+            cmd = ["rocprofv3", *prof, "--output-format", "csv", "-d", str(directory), "-o", "run", "--"] + cmd
+        shown = " ".join(["python3 -u bench.py", *args] if not prof else
+                         ["rocprofv3", *prof, "--output-format", "csv", "-d", "<dir>", "-o", "run", "--",
+                          "python3 -u bench.py", *args])
+        log(f"profile: {key} {tag}")
+        rc, stdout, stderr = _run_child(cmd, 240)
+        (directory / "stdout.txt").write_text(stdout)
+        (directory / "stderr.txt").write_text(stderr[-20000:])
+        result = _result_line(stdout)
+        # rocprofv3 may exit with a signal after the program has finished and
+        # its files are complete; the program's own result line decides.
+        if result is None:
+            raise RuntimeError(f"{key} {tag}: exit {rc} without a result line; see {directory}/stderr.txt")
+        log(f"profile: {key} {tag} done (exit {rc})")
+        return result, directory, shown
+
+    def counter(key: str, name: str) -> tuple[list[tuple[int, str, float]], str]:
+        _, directory, shown = child(key, name.lower(), ["--pmc", name], 2, 1)
+        return _dispatch_counters(directory, name), shown
+
+    scale = {}
+    calibration = {}
+    for name in ("FETCH_SIZE", "WRITE_SIZE"):
+        values, shown = counter("copy", name)
+        kib = max(v for _, _, v in values)
+        scale[name] = (1 << 30) / (kib * 1024.0)
+        calibration[name] = {"kib_per_1GiB_copy": kib, "scale": round(scale[name], 4), "command": shown}
+
+    record = read_traffic()
+    workloads = record.get("workloads", {}) if record.get("sources") == digest else {}
+    for key in keys:
+        cls = WORKLOADS[key]
+        plain, _, plain_cmd = child(key, "plain", [], steps, warmup)
+        traced, directory, trace_cmd = child(key, "trace", ["--kernel-trace", "--stats"], steps, warmup)
+        trace = sorted(_csv_rows(directory, "kernel_trace.csv"), key=lambda r: int(r["Start_Timestamp"]))
+        per_step = traced["kernels_per_step"] or 0
+        n_timed = traced["steps_timed"]
+        timed = trace[-per_step * n_timed:] if per_step else []
+        durations = [(r["Kernel_Name"], (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3) for r in timed]
+        dominant = [d for name, d in durations if cls.kernel in name]
+        kernel_name = next((name for name, _ in durations if cls.kernel in name), cls.kernel)
+        per_step_us = sum(d for _, d in durations) / max(n_timed, 1)
+        stats = sorted(_csv_rows(directory, "kernel_stats.csv"), key=lambda r: -float(r["TotalDurationNs"]))[:6]
+
+        traffic = {}
+        commands = {}
+        for name in ("FETCH_SIZE", "WRITE_SIZE"):
+            values, commands[name] = counter(key, name)
+            mine = [v for _, kernel, v in values if cls.kernel in kernel]
+            mine = mine[-2 * cls_launches(plain):] or mine
+            traffic[name] = statistics.mean(mine) * 1024.0 * scale[name] if mine else None
+        short = short_kernel(kernel_name)
+        entry = {"kernel": short, "launches_per_step": cls_launches(plain),
+                 "fetch_bytes": round(traffic["FETCH_SIZE"]) if traffic["FETCH_SIZE"] else None,
+                 "write_bytes": round(traffic["WRITE_SIZE"]) if traffic["WRITE_SIZE"] else None}
+        entry["bytes_per_launch"] = (entry["fetch_bytes"] + entry["write_bytes"]
+                                     if entry["fetch_bytes"] is not None and entry["write_bytes"] is not None
+                                     else None)
+        if plain.get("work_per_launch") and plain["unit"] == "GB/s":
+            entry["algorithmic_bytes_per_launch"] = round(plain["work_per_launch"])
+        workloads[key] = entry
+
+        lines = [
+            f"# `{short}` — {cls.name}",
+            "",
+            f"Kernel sources digest `{digest}` (bench.py `sources_digest`).  Commands, from the repository root "
+            "on one MI355X (this summary: `python3 bench.py --profile <dir> --only " + key + "`):",
+            "",
+            f"    {plain_cmd}",
+            f"    {trace_cmd}",
+            f"    {commands['FETCH_SIZE']}",
+            f"    {commands['WRITE_SIZE']}",
+            "",
+            "| Figure | Value |",
+            "|---|---|",
+            f"| bench, plain run: median ms per step ({steps} steps) | {plain['ms_per_step']} |",
+            f"| bench, plain run: µs per launch of the dominant kernel (step ÷ {cls_launches(plain)}) | "
+            f"{plain['ms_per_step'] * 1e3 / cls_launches(plain):.2f} |",
+            f"| bench inside the traced run: median ms per step | {traced['ms_per_step']} |",
+            f"| profiler overhead (traced ÷ plain − 1) | {traced['ms_per_step'] / plain['ms_per_step'] - 1:+.1%} |",
+            f"| trace, timed steps: `{short}` launches, mean / min / max µs | {len(dominant)}, "
+            + (f"{statistics.mean(dominant):.2f} / {min(dominant):.2f} / {max(dominant):.2f} |"
+               if dominant else "— |"),
+            f"| trace, timed steps: kernel time per step, all kernels (ms) | {per_step_us / 1e3:.4f} "
+            f"(≤ {traced['ms_per_step_mean']} mean ms per step of the same run: "
+            f"{'yes' if per_step_us / 1e3 <= traced['ms_per_step_mean'] * 1.001 else 'no'}) |",
+            f"| FETCH_SIZE per launch (scaled ×{scale['FETCH_SIZE']:.3f}) | "
+            f"{entry['fetch_bytes'] / 1e6 if entry['fetch_bytes'] else float('nan'):.2f} MB |",
+            f"| WRITE_SIZE per launch (scaled ×{scale['WRITE_SIZE']:.3f}) | "
+            f"{entry['write_bytes'] / 1e6 if entry['write_bytes'] else float('nan'):.2f} MB |",
+        ]
+        if "algorithmic_bytes_per_launch" in entry:
+            lines.append(f"| algorithmic bytes per launch | {entry['algorithmic_bytes_per_launch'] / 1e6:.2f} MB |")
+        lines += ["", "Kernel stats of the traced run (every launch, warm-up and untimed runs included):", "",
+                  "| Kernel | Calls | Average µs | Min µs | Max µs |", "|---|---|---|---|---|"]
+        for row in stats:
+            lines.append(f"| `{row['Name'][:110]}` | {row['Calls']} | {float(row['AverageNs']) / 1e3:.2f} | "
+                         f"{float(row['MinNs']) / 1e3:.2f} | {float(row['MaxNs']) / 1e3:.2f} |")
+        (summaries / f"{short}_{key}.md").write_text("\n".join(lines) + "\n")
+
+    block = {"sources": digest, "calibration": calibration, "workloads": workloads}
+    table = ["| Workload | Kernel | FETCH MB | WRITE MB | Per launch MB | Algorithmic MB |", "|---|---|---|---|---|---|"]
+    for key, e in sorted(workloads.items()):
+        alg = e.get("algorithmic_bytes_per_launch")
+        table.append(f"| {key} | `{e['kernel']}` | {(e['fetch_bytes'] or 0) / 1e6:.2f} | "
+                     f"{(e['write_bytes'] or 0) / 1e6:.2f} | {(e['bytes_per_launch'] or 0) / 1e6:.2f} | "
+                     f"{alg / 1e6 if alg else float('nan'):.2f} |")
+    text = "\n".join([
+        "# HBM traffic per launch of each workload's dominant kernel",
+        "",
+        "FETCH_SIZE and WRITE_SIZE (KiB per dispatch, one rocprofv3 `--pmc` pass each, mean over the last two "
+        "steps' launches), scaled by what the same counter reads for a 1 GiB device copy "
+        f"(FETCH ×{scale['FETCH_SIZE']:.3f}, WRITE ×{scale['WRITE_SIZE']:.3f}).  Made by "
+        "`python3 bench.py --profile <dir>`; bench.py uses these figures only while the kernel sources hash "
+        f"to `{digest}`.",
+        "",
+        *table,
+        "",
+        "```json",
+        json.dumps(block, indent=1),
+        "```",
+        "",
+    ])
+    (summaries / "hbm_traffic.md").write_text(text)
+    log(f"profile: wrote {summaries}")
+    return 0
+
+
+def short_kernel(name: str) -> str:
+    """``void ns::(anonymous namespace)::fwd_ring_kernel<...>(...)`` -> ``fwd_ring_kernel``."""
+    depth, kept = 0, []
+    for ch in name:
+        if ch in "<(":
+            depth += 1
+        if depth == 0:
+            kept.append(ch)
+        if ch in ">)":
+            depth -= 1
+    return "".join(kept).split()[-1].split("::")[-1] if "".join(kept).split() else name
+
+
+def cls_launches(result: dict) -> int:
+    return result["roofline"]["launches_per_step"] if result.get("roofline") else 1
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--no-cpu-baseline", action="store_true")
-    parser.add_argument("--only", choices=["sensevoice", "sensevoice-fsmn", "turbo", "qwen3", "qwen3-paged",
-                                           "qwen3-fused", "qwen3-prefill", "whisper-small", "choice",
-                                           "qwen3-audio", "gemma4-audio", "gemma4-decode", "gemma4-prefill", "copy"],
-                        default=None,
-                        help="measure one workload only (for profiling)")
+    parser.add_argument("--only", default=None,
+                        help="comma-separated workloads to measure alone: " + ", ".join(WORKLOADS))
+    parser.add_argument("--no-compare", action="store_true",
+                        help="with --only: skip the unfused/reference comparison runs")
+    parser.add_argument("--profile", metavar="DIR", default=None,
+                        help="rocprofv3 trace and counter runs of the workloads, summaries under DIR/profiles")
     parser.add_argument("--sweep", action="store_true",
                         help="time the encoder kernel over a table of shapes (one launch per line)")
     args = parser.parse_args()
@@ -1017,6 +1611,14 @@ def main() -> int:
             file=sys.stderr,
         )
         return 2
+    keys = args.only.split(",") if args.only else None
+    for key in keys or []:
+        if key not in WORKLOADS:
+            print(f"unknown workload {key!r}; one of {', '.join(WORKLOADS)}", file=sys.stderr)
+            return 2
+    if args.profile:
+        chosen = keys or ["sensevoice", *(k for group in GROUPS.values() for k in group)]
+        return profile(Path(args.profile), chosen, args.steps, args.warmup)
 
     import torch
 
@@ -1029,48 +1631,34 @@ def main() -> int:
     if args.sweep:
         shape_sweep(torch, attention)
         return 0
-    selected = {
-        "sensevoice": SenseVoiceEncoder,
-        "sensevoice-fsmn": SenseVoiceAttentionFsmn,
-        "turbo": WhisperTurboEncoder,
-        "qwen3": Qwen3Decode,
-        "qwen3-paged": Qwen3DecodePaged,
-        "qwen3-fused": Qwen3DecodeStepFused,
-        "qwen3-prefill": Qwen3Prefill,
-        "qwen3-audio": Qwen3AudioAttention,
-        "gemma4-audio": Gemma4AudioAttention,
-        "gemma4-decode": Gemma4TextDecode,
-        "gemma4-prefill": Gemma4Prefill,
-        "choice": GreedyChoice,
-        "whisper-small": WhisperSmallDecoderStep,
-        "copy": CopyCalibration,
-    }
-    if args.only:
-        workload = selected[args.only](torch, attention)
-        result = measure(torch, workload, args.steps, args.warmup)
-        log(json.dumps(result))
-        print(json.dumps(result))
+
+    def run(key: str, compare: bool = True) -> dict:
+        log(f"bench: {key}")
+        workload = WORKLOADS[key](torch, attention)
+        result = measure(torch, workload, key, args.steps, args.warmup, compare)
+        del workload
+        torch.cuda.empty_cache()
+        return result
+
+    if keys:
+        for key in keys:
+            result = run(key, compare=not args.no_compare)
+            if not args.no_cpu_baseline and key in CPU_BASELINES:
+                result["cpu_baseline"] = cpu_baseline(key, 5.0)
+            print(json.dumps(result), flush=True)
         return 0
 
-    log("bench: sensevoice encoder attention")
-    head = measure(torch, SenseVoiceEncoder(torch, attention), args.steps, args.warmup)
-    torch.cuda.empty_cache()
-    decode = []
-    for cls in (Qwen3Decode, Qwen3DecodePaged, Qwen3DecodeStepFused, WhisperSmallDecoderStep, GreedyChoice,
-                Gemma4TextDecode):
-        log(f"bench: {cls.name}")
-        decode.append(measure(torch, cls(torch, attention), args.steps, args.warmup))
-        torch.cuda.empty_cache()
-    secondary = []
-    for cls in (SenseVoiceAttentionFsmn, WhisperTurboEncoder, Qwen3Prefill, Qwen3AudioAttention, Gemma4AudioAttention,
-                Gemma4Prefill):
-        log(f"bench: {cls.name}")
-        secondary.append(measure(torch, cls(torch, attention), args.steps, args.warmup))
-        torch.cuda.empty_cache()
+    head = run("sensevoice")
+    groups = {name: [run(key) for key in group] for name, group in GROUPS.items()}
     baseline = None
     if not args.no_cpu_baseline:
-        log("bench: cpu baseline")
-        baseline = cpu_baseline()
+        log("bench: cpu baselines")
+        baseline = cpu_baseline("sensevoice", 8.0)
+        for lines in groups.values():
+            for result in lines:
+                key = next(k for k, cls in WORKLOADS.items() if cls.name == result["workload"])
+                if key in CPU_BASELINES:
+                    result["cpu_baseline"] = cpu_baseline(key, 5.0)
 
     line = {
         "metric": METRIC,
@@ -1088,8 +1676,8 @@ def main() -> int:
         "config": head["config"],
         "roofline": head["roofline"],
         "cpu_baseline": baseline,
-        "decode": decode,
-        "secondary": secondary,
+        "ms_per_step_mean": head["ms_per_step_mean"],
+        **groups,
     }
     print(json.dumps(line), flush=True)
     return 0
