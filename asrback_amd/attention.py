@@ -27,12 +27,20 @@ write) and :func:`greedy_choice` (argmax and its log-probability).
 The reference's masks are all prefix masks: each query row sees keys
 ``0 .. n-1`` (optionally causal on top).  A boolean mask with a hole is
 refused (:meth:`KeyPrefix.from_mask`).
+
+Split-K decode and the split greedy choice keep partials in a workspace the
+caller owns: a decoder sizes one buffer at its largest bucket
+(:func:`decode_workspace_size`, :func:`choice_workspace_size`) and runs its
+steps inside :func:`workspace`; calls outside any take a stream-ordered
+temporary.
 """
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import math
+import threading
 from dataclasses import dataclass
 
 import torch
@@ -433,7 +441,8 @@ def decode(
     cache), or with ``pages`` the pools ``(num_pages, page_size, heads_kv,
     head_dim)``.  Sequence ``b`` uses keys ``0 .. n_b - 1`` with ``n_b =
     seqused_k[b]`` (int32), ``positions[b] + 1`` (int64) or ``length``.
-    ``workspace`` defaults to the device's shared one.  Returns ``(batch, heads_q, head_dim)``.
+    ``workspace``: the split partials' memory (see :func:`workspace`).
+    Returns ``(batch, heads_q, head_dim)``.
     """
     if q.dim() != 3 or k.dim() != 4 or v.shape != k.shape:
         raise ValueError(
@@ -467,12 +476,8 @@ def decode(
         pk, params.max_len_k = _paged(pages, k, v, q.shape[0])
         params.k_batch_stride = params.v_batch_stride = 0
     lib = _lib.load()
-    need = lib.asrattn_decode_workspace_size(ctypes.byref(params))
-    if need == ctypes.c_size_t(-1).value:
-        need = 0  # invalid parameters: the call below reports why
-    if workspace is None and need:
-        workspace = decode_workspace(need, device)
-    size = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    workspace = _split_workspace(lib.asrattn_decode_workspace_size(ctypes.byref(params)), workspace, device)
+    size = 0 if workspace is None else workspace.numel()
     if pk is None:
         status = lib.asrattn_decode(ctypes.byref(params), _ptr(workspace), size, _stream(device))
         _lib.check(status, "asrattn_decode")
@@ -574,10 +579,8 @@ def decode_append(
     app.rope_batch_stride = 0 if cos is None else cos.stride(0)
     app.v_norm = 1 if v_norm else 0
     lib = _lib.load()
-    need = lib.asrattn_decode_workspace_size(ctypes.byref(params))
-    if workspace is None and need and need != ctypes.c_size_t(-1).value:
-        workspace = decode_workspace(need, device)
-    size = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    workspace = _split_workspace(lib.asrattn_decode_workspace_size(ctypes.byref(params)), workspace, device)
+    size = 0 if workspace is None else workspace.numel()
     if pk is None:
         status = lib.asrattn_decode_append(ctypes.byref(params), ctypes.byref(app), _ptr(workspace), size,
                                            _stream(device))
@@ -645,16 +648,16 @@ def local_attention(
     return out
 
 
-def greedy_choice(logits: Tensor, suppress: Tensor | None = None) -> tuple[Tensor, Tensor]:
+def greedy_choice(logits: Tensor, suppress: Tensor | None = None, *,
+                  workspace: Tensor | None = None) -> tuple[Tensor, Tensor]:
     """Greedy next token per row of float32 ``logits`` ``(rows, vocab)`` and
     its log-probability, in one pass (``asrattn_choose``): the argmax (first
     index among equal maxima) after setting ``suppress``-ed entries (bool or
     uint8 ``(vocab,)``) to -inf, and ``log_softmax`` at it.  Replaces the
     greedy path of ``whisper.py:962-974`` and ``qwen3_asr.py:1200-1210``;
     ``logits`` is not modified.  Returns int64 tokens and float32
-    log-probabilities ``(rows,)``.  Rows are split over several workgroups
-    through the device's decode workspace (a fixed address, so a captured
-    graph replays it)."""
+    log-probabilities ``(rows,)``.  Rows are split over several workgroups,
+    their partials in ``workspace`` (see :func:`workspace`)."""
     if logits.dim() != 2 or logits.dtype != torch.float32:
         raise ValueError("greedy_choice takes float32 (rows, vocab) logits")
     if logits.stride(-1) != 1:
@@ -670,21 +673,14 @@ def greedy_choice(logits: Tensor, suppress: Tensor | None = None) -> tuple[Tenso
     token = torch.empty(rows, dtype=torch.int64, device=device)
     logprob = torch.empty(rows, dtype=torch.float32, device=device)
     lib = _lib.load()
-    need = lib.asrattn_choose_workspace_size(rows, vocab)
-    workspace = decode_workspace(need, device) if need else None
-    size = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    workspace = _split_workspace(lib.asrattn_choose_workspace_size(rows, vocab), workspace, device)
+    size = 0 if workspace is None else workspace.numel()
     _lib.check(
         lib.asrattn_choose(logits.data_ptr(), rows, vocab, logits.stride(0), _ptr(suppress), token.data_ptr(),
                            logprob.data_ptr(), _ptr(workspace), size, _stream(device)),
         "asrattn_choose",
     )
     return token, logprob
-
-
-# Decode workspaces per device: one buffer serves every call on the device
-# (calls on one device run in stream order); grown buffers are kept alive
-# because graphs captured earlier still hold their addresses.
-_workspaces: dict[torch.device, list[Tensor]] = {}
 
 
 def decode_supported(dtype: torch.dtype, head_dim: int, group: int) -> bool:
@@ -695,20 +691,70 @@ def decode_supported(dtype: torch.dtype, head_dim: int, group: int) -> bool:
     return dtype in _DTYPES and head_dim in sizes and group in (1, 2, 4, 8)
 
 
-def decode_workspace(nbytes: int, device: torch.device) -> Tensor:
-    """A decode workspace of at least ``nbytes`` on ``device``, shared by
-    every :func:`decode` on that device (calls on one device must not run
-    concurrently on different streams)."""
-    device = torch.device(device)
-    if device.index is None:
-        device = torch.device(device.type, torch.cuda.current_device())
-    held = _workspaces.setdefault(device, [])
-    if held and held[-1].numel() >= nbytes:
-        return held[-1]
-    size = max(nbytes, 2 * held[-1].numel() if held else 1 << 20)
-    buffer = torch.empty(size, dtype=torch.uint8, device=device)
-    held.append(buffer)
+_scope = threading.local()
+
+
+@contextlib.contextmanager
+def workspace(buffer: Tensor):
+    """Use ``buffer`` -- caller-owned uint8 device memory -- for the split
+    partials of every :func:`decode`, :func:`decode_append` and
+    :func:`greedy_choice` call of this thread inside the block that passes
+    no ``workspace`` of its own.  Size it once, at the largest shape the
+    block runs (:func:`decode_workspace_size`,
+    :func:`choice_workspace_size`); a call that needs more raises.  Its
+    address stays fixed, so graphs captured inside the block replay it.
+    Calls that share one buffer must run in stream order.
+
+    Without a buffer, each call that splits takes a temporary from torch's
+    caching allocator (stream-ordered; inside graph capture, from the
+    graph's pool)."""
+    if buffer.dtype != torch.uint8 or buffer.dim() != 1 or not buffer.is_contiguous():
+        raise ValueError("a workspace is a contiguous 1-D uint8 tensor")
+    previous = getattr(_scope, "buffer", None)
+    _scope.buffer = buffer
+    try:
+        yield buffer
+    finally:
+        _scope.buffer = previous
+
+
+def _split_workspace(need: int, given: Tensor | None, device: torch.device) -> Tensor | None:
+    """The workspace of a call that needs ``need`` bytes: ``given``, else the
+    thread's :func:`workspace` buffer, else a temporary."""
+    if need == 0 or need == ctypes.c_size_t(-1).value:
+        return given  # no split (or invalid parameters: the call reports why)
+    buffer = given if given is not None else getattr(_scope, "buffer", None)
+    if buffer is None:
+        return torch.empty(need, dtype=torch.uint8, device=device)
+    if buffer.dtype != torch.uint8 or buffer.dim() != 1 or not buffer.is_contiguous():
+        raise ValueError("a workspace is a contiguous 1-D uint8 tensor")
+    if buffer.device != device:
+        raise ValueError(f"the workspace is on {buffer.device}, the call on {device}")
+    if buffer.numel() < need:
+        raise ValueError(f"the call needs {need} workspace bytes, the workspace holds {buffer.numel()}")
     return buffer
+
+
+def decode_workspace_size(batch: int, heads_q: int, heads_kv: int, head_dim: int, max_len_k: int,
+                          dtype: torch.dtype = torch.bfloat16, num_splits: int = 0) -> int:
+    """Bytes of split partials a :func:`decode` / :func:`decode_append` call
+    of these sizes needs (``asrattn_decode_workspace_size``; 0 when it runs
+    unsplit).  Raises for sizes the library does not take."""
+    params = _lib.DecodeParams()
+    params.batch, params.heads_q, params.heads_kv, params.head_dim = batch, heads_q, heads_kv, head_dim
+    params.max_len_k, params.num_splits, params.scale = max_len_k, num_splits, 1.0
+    params.dtype = _lib.BF16 if dtype == torch.bfloat16 else _lib.F32
+    lib = _lib.load()
+    need = lib.asrattn_decode_workspace_size(ctypes.byref(params))
+    if need == ctypes.c_size_t(-1).value:
+        raise ValueError(lib.asrattn_last_error().decode("utf-8", "replace"))
+    return int(need)
+
+
+def choice_workspace_size(rows: int, vocab: int) -> int:
+    """Bytes of partials :func:`greedy_choice` over ``(rows, vocab)`` logits
+    needs (``asrattn_choose_workspace_size``)."""
+    return int(_lib.load().asrattn_choose_workspace_size(rows, vocab))
 
 
 def sdpa(

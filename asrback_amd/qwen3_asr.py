@@ -36,6 +36,7 @@ import torch
 import torch.nn.functional as F
 from torch import Tensor, nn
 
+from . import attention
 from .attention import KeyPrefix, PageTable, decode, decode_append, greedy_choice, varlen_attn
 from .transcription import CapturedGraph, to_device
 
@@ -474,10 +475,25 @@ class TextGreedyDecoder:
             self.cache = PagedKVCache.allocate(config, max_batch_size, pages, page_size, self.device, self.dtype)
         self.state = DecodeState.allocate(max_batch_size, self.device)
         self.eos_ids = torch.tensor(eos_ids, dtype=torch.long, device=self.device)
+        self.workspace = torch.empty(self._workspace_bytes(), dtype=torch.uint8, device=self.device)
         self.rows: dict[int, dict] = {}
         self.graphs: dict[tuple[int, int], CapturedGraph] = {}
         if graphs:
             self._capture_graphs()
+
+    def _workspace_bytes(self) -> int:
+        """Split partials of the largest step over the buckets: the decode
+        launch per layer and the greedy choice over the logits."""
+        config = self.config
+        vocab = self.lm_head.weight.shape[0]
+        need = 256
+        for batch in self.buckets:
+            for length in self.kv_buckets:
+                need = max(need, attention.decode_workspace_size(
+                    batch, config["num_attention_heads"], config["num_key_value_heads"], config["head_dim"],
+                    length, self.dtype))
+            need = max(need, attention.choice_workspace_size(batch, vocab))
+        return need
 
     @torch.inference_mode()
     def _capture_graphs(self) -> None:
@@ -540,7 +556,8 @@ class TextGreedyDecoder:
         hidden = self.text.prefill(x, self.cache, rows, positions_d, segments,
                                    self.cos[positions_d], self.sin[positions_d])
         last = segments.starts[1:].long() - 1
-        token, logprob = choose(self.logits(hidden[last]), temperatures)
+        with attention.workspace(self.workspace):
+            token, logprob = choose(self.logits(hidden[last]), temperatures)
         state = self.state
         state.tokens[slot_rows] = token
         state.position[slot_rows] = start
@@ -554,9 +571,11 @@ class TextGreedyDecoder:
 
     def step(self, state: DecodeState, cache: KVCache, temperatures: Tensor | None = None) -> None:
         """Decode ``state.tokens`` and select every row's next token
-        (``qwen3_asr.py:1179-1198``)."""
-        hidden = self.text.step(state.tokens, state.position, cache, self.cos, self.sin)
-        token, logprob = choose(self.logits(hidden), temperatures)
+        (``qwen3_asr.py:1179-1198``).  Split partials go to the decoder's
+        own workspace, sized at construction for the largest bucket."""
+        with attention.workspace(self.workspace):
+            hidden = self.text.step(state.tokens, state.position, cache, self.cos, self.sin)
+            token, logprob = choose(self.logits(hidden), temperatures)
         active = ~state.finished
         position = state.position + active
         token = torch.where(active, token, state.tokens)

@@ -30,6 +30,7 @@ import torch
 import torch.nn.functional as F
 from torch import Tensor, nn
 
+from . import attention
 from .attention import KeyPrefix, decode_append, greedy_choice, sdpa
 from .transcription import CapturedGraph, to_device
 
@@ -386,10 +387,26 @@ class GreedyDecoder:
         self.cache = model.allocate_cache(max_batch_size)
         self.staging = model.allocate_cache(max_batch_size)
         self.state = DecodeState.allocate(max_batch_size, max_target, self.device)
+        self.workspace = torch.empty(self._workspace_bytes(), dtype=torch.uint8, device=self.device)
         self.rows: dict[int, dict] = {}
         self.graphs: dict[tuple[int, int], CapturedGraph] = {}
         if graphs:
             self._capture_graphs()
+
+    def _workspace_bytes(self) -> int:
+        """Split partials of the largest step over the buckets: each layer's
+        self-attention over its KV bucket and cross-attention over the
+        encoder frames, and the greedy choice over the logits."""
+        config = self.config
+        heads = config["decoder_attention_heads"]
+        head_dim = config["d_model"] // heads
+        dtype = self.model.model.decoder.embed_tokens.weight.dtype
+        need = 256
+        for batch in self.buckets:
+            for length in [*self.kv_buckets, config["max_source_positions"]]:
+                need = max(need, attention.decode_workspace_size(batch, heads, heads, head_dim, length, dtype))
+            need = max(need, attention.choice_workspace_size(batch, config["vocab_size"]))
+        return need
 
     @torch.inference_mode()
     def _capture_graphs(self) -> None:
@@ -424,7 +441,8 @@ class GreedyDecoder:
         tokens = to_device(prefixes, self.device)
         hidden = self.model.decode(tokens, self._positions[:prefix_length], staging, length=prefix_length)
         logits = self.model.logits(hidden[:, -1:]).float()[:, 0]
-        token, logprob = choose(logits, self._first_suppress)
+        with attention.workspace(self.workspace):
+            token, logprob = choose(logits, self._first_suppress)
         available = self.config["max_target_positions"] - prefix_length
         end = prefix_length - 1 + min(max_new_tokens, available)
         rows = to_device(slots, self.device)
@@ -441,10 +459,13 @@ class GreedyDecoder:
         return slots
 
     def step(self, state: DecodeState, cache: DecoderCache) -> None:
-        """One greedy step for every row (``whisper.py:942-960``)."""
-        hidden = self.model.decode(state.tokens, state.position, cache)
-        logits = self.model.logits(hidden[:, -1]).float()
-        token, logprob = choose(logits, self._suppress)
+        """One greedy step for every row (``whisper.py:942-960``); split
+        partials go to the decoder's own workspace, sized at construction for
+        the largest bucket."""
+        with attention.workspace(self.workspace):
+            hidden = self.model.decode(state.tokens, state.position, cache)
+            logits = self.model.logits(hidden[:, -1]).float()
+            token, logprob = choose(logits, self._suppress)
         active = ~state.finished
         position = state.position + active
         token = torch.where(active, token, state.tokens[:, 0])

@@ -160,3 +160,38 @@ def test_paged_layer_write_skips_rows_without_pages():
     assert torch.equal(cache.pool_keys[0, 2, 0], torch.full((2, 8), 7.0))
     assert not (cache.pool_keys[0, :3] == -5.0).any()  # the free row's write went to the sink page
 
+
+
+def test_workspace_sizes_and_scoped_buffer():
+    """Split-K workspace sizing through the C ABI, and the caller-owned
+    buffer a ``workspace`` block installs (checked before any device call)."""
+    from asrback_amd import attention
+
+    # 64 rows x 8 kv heads fill the GPU without splits; one row over 4096
+    # keys splits (16 query heads x splits x 128 floats, plus the maxima and
+    # sums).
+    assert attention.decode_workspace_size(64, 16, 8, 128, 1024) == 0
+    one = attention.decode_workspace_size(1, 16, 8, 128, 4096)
+    assert one >= 16 * 16 * 128 * 4 and one % 256 == 0
+    assert attention.decode_workspace_size(1, 16, 8, 128, 4096, num_splits=2) < one
+    with pytest.raises(ValueError):
+        attention.decode_workspace_size(1, 16, 8, 96, 4096)  # no kernel for head_dim 96
+    assert attention.choice_workspace_size(64, 151936) > 0
+
+    device = torch.device("cpu")
+    small = torch.empty(64, dtype=torch.uint8)
+    big = torch.empty(1 << 16, dtype=torch.uint8)
+    assert attention._split_workspace(0, None, device) is None
+    temporary = attention._split_workspace(1000, None, device)
+    assert temporary.numel() == 1000 and temporary.dtype == torch.uint8
+    with attention.workspace(big):
+        assert attention._split_workspace(1000, None, device) is big
+        assert attention._split_workspace(1000, small.new_empty(2000), device).numel() == 2000
+        with attention.workspace(small):
+            with pytest.raises(ValueError, match="needs 1000 workspace bytes"):
+                attention._split_workspace(1000, None, device)
+        assert attention._split_workspace(1000, None, device) is big
+    assert attention._split_workspace(1000, None, device) is not big
+    with pytest.raises(ValueError):
+        with attention.workspace(torch.empty(8, dtype=torch.float32)):
+            pass
