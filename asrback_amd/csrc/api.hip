@@ -175,6 +175,9 @@ int run_fwd(const asrattn_fwd_params& p, const asrattn::FsmnArgs* fsmn, void* st
     const bool fused = fsmn != nullptr && fsmn->kernel_size <= asrattn::kFsmnFusedKernel;
     err = asrattn::launch_fwd_ring(p, fused ? fsmn : nullptr, s);
     if (fused || fsmn == nullptr || err != hipSuccess) return from_hip(err, name);
+  } else if (!generic && asrattn::fwd_f32mm_supported(p)) {
+    err = asrattn::launch_fwd_f32mm(p, s);
+    if (fsmn == nullptr || err != hipSuccess) return from_hip(err, name);
   } else {
     err = asrattn::launch_fwd_valu(p, s);
     if (fsmn == nullptr || err != hipSuccess) return from_hip(err, name);

@@ -40,6 +40,11 @@ size_t choose_workspace_bytes(int64_t rows, int64_t vocab);
 hipError_t launch_choose(const float* logits, int64_t rows, int64_t vocab, int64_t row_stride, const uint8_t* suppress,
                          int64_t* token, float* logprob, void* workspace, hipStream_t stream);
 
+// Multi-row forward in fp32 on the matrix cores (head_dim 64 or 128, no
+// sliding window, K/V spans addressable with 32-bit offsets).
+hipError_t launch_fwd_f32mm(const asrattn_fwd_params& p, hipStream_t stream);
+bool fwd_f32mm_supported(const asrattn_fwd_params& p);
+
 // Multi-row forward on the vector ALUs (fp32 or bf16, head_dim 64 or 128):
 // the fp32 path, the fallback for bf16 layouts the matrix-core kernel does
 // not address, and the reference-precision check of that kernel.
