@@ -522,9 +522,10 @@ class Gemma4TextDecode(Workload):
 
 class Qwen3Decode(Workload):
     """Qwen3-ASR-1.7B GQA decoder step (qwen3_asr.py:392-432): q ``(64, 16,
-    128)`` over the ``(28, 64, 1024, 8, 128)`` cache, ``seqused_k =
-    position + 1``; each step advances every row by one position, 128 steps
-    from prompts of 390 + U{10..40} tokens."""
+    128)`` over the ``(28, 64, 1024, 8, 128)`` cache, keys ``0 ..
+    position`` (the kernel reads the positions, as the decoders pass them);
+    each step advances every row by one position, 128 steps from prompts of
+    390 + U{10..40} tokens."""
 
     name = "qwen3-asr-1.7b-decode-attention"
     unit = "GB/s"
@@ -564,9 +565,10 @@ class Qwen3Decode(Workload):
 
     def run(self) -> None:
         self.positions.add_(1)
-        self.used.copy_(self.positions + 1)  # seqused_k = position + 1 (int32)
+        # Keys 0 .. position: the kernel reads the positions, as the decoders
+        # pass them (KeyPrefix(positions=...)); no separate length tensor.
         for layer in range(self.layers):
-            self.attention.decode(self.q[layer], self.keys[layer], self.values[layer], seqused_k=self.used,
+            self.attention.decode(self.q[layer], self.keys[layer], self.values[layer], positions=self.positions,
                                   out=self.out)
 
     def config(self) -> dict:
@@ -603,9 +605,8 @@ class Qwen3DecodePaged(Qwen3Decode):
 
     def run(self) -> None:
         self.positions.add_(1)
-        self.used.copy_(self.positions + 1)
         for layer in range(self.layers):
-            self.attention.decode(self.q[layer], self.keys[layer], self.values[layer], seqused_k=self.used,
+            self.attention.decode(self.q[layer], self.keys[layer], self.values[layer], positions=self.positions,
                                   out=self.out, pages=self.pages)
 
     def config(self) -> dict:
