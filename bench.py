@@ -69,6 +69,7 @@ sys.path.insert(0, str(ROOT))
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PEAK_FP32_TFLOPS = 157.3  # MI355X dense fp32 matrix
 PEAK_HBM_GBS = 8000.0  # MI355X HBM3E
+MFMA_FILE = ROOT / "profiles" / "mfma_utilisation.md"
 TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic.md"
 METRIC = "attn TFLOP/s (encoder) & HBM GB/s (decode step), % of MI355X roofline"
 
@@ -1017,10 +1018,10 @@ def sources_digest() -> str:
     return h.hexdigest()[:16]
 
 
-def read_traffic() -> dict:
-    """The JSON block of profiles/hbm_traffic.md ({} when absent)."""
+def read_traffic(path: Path | None = None) -> dict:
+    """The JSON block of profiles/hbm_traffic.md, or of ``path`` ({} when absent)."""
     try:
-        text = TRAFFIC_FILE.read_text()
+        text = (path or TRAFFIC_FILE).read_text()
         return json.loads(text.split("```json", 1)[1].split("```", 1)[0])
     except (OSError, IndexError, ValueError):
         return {}
@@ -1472,8 +1473,17 @@ def profile(out: Path, keys: list[str], steps: int, warmup: int) -> int:
         scale[name] = (1 << 30) / (kib * 1024.0)
         calibration[name] = {"kib_per_1GiB_copy": kib, "scale": round(scale[name], 4), "command": shown}
 
-    record = read_traffic()
+    # Earlier --profile calls into the same directory (same sources) merge,
+    # else the committed table does.
+    record = read_traffic(summaries / "hbm_traffic.md")
+    if record.get("sources") != digest:
+        record = read_traffic()
     workloads = record.get("workloads", {}) if record.get("sources") == digest else {}
+    mfma = read_traffic(summaries / MFMA_FILE.name)
+    mfma_rows = mfma.get("workloads", {}) if mfma.get("sources") == digest else {}
+    mfma_counters = ["SQ_VALU_MFMA_BUSY_CYCLES", "SQ_VALU_MFMA_COEXEC_CYCLES", "SQ_INSTS_MFMA", "SQ_INSTS_VALU",
+                     "GRBM_GUI_ACTIVE"]
+    mfma_command = None
     for key in keys:
         cls = WORKLOADS[key]
         plain, _, plain_cmd = child(key, "plain", [], steps, warmup)
@@ -1505,6 +1515,28 @@ def profile(out: Path, keys: list[str], steps: int, warmup: int) -> int:
         if plain.get("work_per_launch") and plain["unit"] == "GB/s":
             entry["algorithmic_bytes_per_launch"] = round(plain["work_per_launch"])
         workloads[key] = entry
+
+        if cls.bound == "mfma":
+            # One counter pass: matrix-core busy and VALU co-execution cycles,
+            # per dispatch of the dominant kernel (mean over the last two steps).
+            _, mdir, mfma_command = child(key, "mfma", ["--pmc", *mfma_counters], 2, 1)
+            per = {}
+            for name in mfma_counters:
+                vals = [v for _, kernel, v in _dispatch_counters(mdir, name) if cls.kernel in kernel]
+                vals = vals[-2 * cls_launches(plain):] or vals
+                per[name] = statistics.mean(vals) if vals else None
+            if all(per.get(n) for n in ("SQ_VALU_MFMA_BUSY_CYCLES", "GRBM_GUI_ACTIVE", "SQ_INSTS_MFMA")):
+                cycles = per["GRBM_GUI_ACTIVE"] / 8  # summed over the 8 XCDs
+                mfma_rows[key] = {
+                    "kernel": short_kernel(kernel_name),
+                    "mfma_busy": round(per["SQ_VALU_MFMA_BUSY_CYCLES"] / (cycles * 1024), 4),
+                    "coexec_of_busy": round((per["SQ_VALU_MFMA_COEXEC_CYCLES"] or 0) /
+                                            per["SQ_VALU_MFMA_BUSY_CYCLES"], 4),
+                    "valu_per_mfma": round(((per["SQ_INSTS_VALU"] or 0) - per["SQ_INSTS_MFMA"]) /
+                                           per["SQ_INSTS_MFMA"], 2),
+                    "mfma_per_dispatch": round(per["SQ_INSTS_MFMA"]),
+                    "us_per_launch": round(statistics.mean(dominant), 2) if dominant else None,
+                }
 
         lines = [
             f"# `{short}` — {cls.name}",
@@ -1568,6 +1600,33 @@ def profile(out: Path, keys: list[str], steps: int, warmup: int) -> int:
         "",
     ])
     (summaries / "hbm_traffic.md").write_text(text)
+    if mfma_rows:
+        rows = ["| Workload | Kernel | µs per launch | MFMA busy | VALU co-executing (share of busy cycles) | "
+                "VALU per MFMA | MFMA per dispatch |", "|---|---|---|---|---|---|---|"]
+        for key, e in sorted(mfma_rows.items()):
+            rows.append(f"| {key} | `{e['kernel']}` | {e['us_per_launch']} | {e['mfma_busy']:.1%} | "
+                        f"{e['coexec_of_busy']:.1%} | {e['valu_per_mfma']} | {e['mfma_per_dispatch']} |")
+        shown = mfma_command or "rocprofv3 --pmc " + " ".join(mfma_counters) + " -- python3 -u bench.py --only <W> ..."
+        (summaries / MFMA_FILE.name).write_text("\n".join([
+            "# Matrix-core utilisation of the encoder kernels",
+            "",
+            "One rocprofv3 counter pass per workload, per dispatch of its dominant kernel (mean over the last "
+            "two steps' launches); made by `python3 bench.py --profile <dir>` with, per workload W:",
+            "",
+            f"    {shown}",
+            "",
+            "MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / 8 XCDs x 1024 SIMDs); co-executing = "
+            "SQ_VALU_MFMA_COEXEC_CYCLES / SQ_VALU_MFMA_BUSY_CYCLES (matrix cycles during which the same SIMD also "
+            "issued vector ALU work); VALU per MFMA = (SQ_INSTS_VALU - SQ_INSTS_MFMA) / SQ_INSTS_MFMA.  "
+            f"Kernel sources digest `{digest}`.",
+            "",
+            *rows,
+            "",
+            "```json",
+            json.dumps({"sources": digest, "workloads": mfma_rows}, indent=1),
+            "```",
+            "",
+        ]))
     log(f"profile: wrote {summaries}")
     return 0
 
