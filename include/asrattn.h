@@ -45,8 +45,10 @@ enum asrattn_status {
 
 enum asrattn_dtype { ASRATTN_F32 = 0, ASRATTN_BF16 = 1 };
 
-/* asrattn_fwd_params.flags: run the fp32 vector-ALU kernel even where the
-   bf16 matrix-core kernel applies (the exact-arithmetic twin, for checks). */
+/* asrattn_fwd_params.flags: run the vector-ALU kernel (fp32 arithmetic on
+   the vector units) even where a matrix-core kernel applies -- the bf16 one,
+   or the fp32 one at head_dim 64/128 -- as the exact-arithmetic twin, for
+   checks. */
 #define ASRATTN_FWD_FORCE_VALU 1
 /* asrattn_fwd_params.flags: padded layout (cu_seqlens NULL), non-causal,
    seqused_k given: query rows t >= seqused_k[b] are not computed and get
