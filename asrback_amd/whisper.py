@@ -338,15 +338,22 @@ class DecodeState:
         self.tokens[rows] = 0
 
 
-def choose(logits: Tensor, suppress: Tensor) -> tuple[Tensor, Tensor]:
-    """Greedy next token per row and its log-probability (``whisper.py:962-974``,
-    temperature 0).  fp32 logits on the GPU take one fused pass
+def choose(logits: Tensor, suppress: Tensor, temperatures: Tensor | None = None) -> tuple[Tensor, Tensor]:
+    """Next token per row -- greedy, or sampled where the row's temperature is
+    positive -- and its log-probability (``whisper.py:962-974``).  All greedy
+    over fp32 logits on the GPU: one fused pass
     (:func:`~asrback_amd.attention.greedy_choice`; ``logits`` stays
-    unmodified), others the reference's ops."""
-    if logits.is_cuda and logits.dtype == torch.float32 and logits.dim() == 2 and suppress.dim() == 1:
+    unmodified).  Otherwise the reference's ops, suppressed tokens filled
+    with -inf in ``logits`` as the reference does."""
+    if (temperatures is None and logits.is_cuda and logits.dtype == torch.float32 and logits.dim() == 2
+            and suppress.dim() == 1):
         return greedy_choice(logits, suppress)
     logits.masked_fill_(suppress, -math.inf)
     token = logits.argmax(dim=-1)
+    if temperatures is not None:
+        scaled = logits / temperatures.clamp(min=1e-6)[:, None]
+        sampled = torch.multinomial(F.softmax(scaled, dim=-1), 1).squeeze(1)
+        token = torch.where(temperatures > 0, sampled, token)
     logprob = F.log_softmax(logits, dim=-1).gather(1, token[:, None]).squeeze(1)
     return token, logprob
 

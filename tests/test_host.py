@@ -195,3 +195,32 @@ def test_workspace_sizes_and_scoped_buffer():
     with pytest.raises(ValueError):
         with attention.workspace(torch.empty(8, dtype=torch.float32)):
             pass
+
+
+def test_whisper_choose_samples_where_temperature_is_positive():
+    """Whisper's choose takes the reference's temperatures (whisper.py:962-974):
+    rows at temperature 0 take the argmax, rows above it sample, suppressed
+    tokens are never chosen, and the log-probability is log_softmax at the
+    chosen token."""
+    import torch
+
+    from asrback_amd.whisper import choose
+
+    g = torch.Generator().manual_seed(5)
+    logits = torch.randn(6, 50, generator=g)
+    suppress = torch.zeros(50, dtype=torch.bool)
+    suppress[[3, 7, 11]] = True
+    temperatures = torch.tensor([0.0, 1.0, 0.0, 2.0, 0.5, 0.0])
+    masked = logits.masked_fill(suppress, float("-inf"))
+    torch.manual_seed(9)
+    token, logprob = choose(logits.clone(), suppress, temperatures)
+    greedy = temperatures == 0
+    assert torch.equal(token[greedy], masked.argmax(dim=-1)[greedy])
+    assert not suppress[token].any()
+    ref_lp = torch.log_softmax(masked, dim=-1).gather(1, token[:, None]).squeeze(1)
+    assert torch.allclose(logprob, ref_lp)
+    # The same seed reproduces the reference's sampling ops exactly.
+    torch.manual_seed(9)
+    scaled = masked / temperatures.clamp(min=1e-6)[:, None]
+    sampled = torch.multinomial(torch.softmax(scaled, dim=-1), 1).squeeze(1)
+    assert torch.equal(token, torch.where(temperatures > 0, sampled, masked.argmax(dim=-1)))
