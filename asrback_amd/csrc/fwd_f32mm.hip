@@ -32,6 +32,7 @@
 #include "common.hpp"
 #include "fwd_common.hpp"
 #include "kernels.hpp"
+#include "ring_common.hpp"
 
 namespace asrattn {
 namespace {
@@ -67,15 +68,19 @@ struct Operands {
 };
 
 template <int HD, int KS, int OCC>
-__global__ __launch_bounds__(64 * KS, OCC) void fwd_f32mm_kernel(const FwdArgs a) {
+__global__ __launch_bounds__(64 * KS, OCC) void fwd_f32mm_kernel(const FwdArgs a, int q_tiles, int total) {
   using S = F32Shape<HD>;
   constexpr int NQ = S::kQ4, DB = S::kDB;
   const asrattn_fwd_params& p = a.p;
-  const int hq = blockIdx.y;
-  const int b = blockIdx.z;
+  // Each XCD takes a contiguous range of (sequence, head, row block) items,
+  // so a head's keys and values stay in that XCD's L2 for all its row blocks.
+  const int item = ring::xcd_remap((int)blockIdx.x, total);
+  const int qt = item % q_tiles;
+  const int hq = (item / q_tiles) % p.heads_q;
+  const int b = item / q_tiles / p.heads_q;
   const int hkv = hq / (p.heads_q / p.heads_kv);
   const SeqView sv = seq_view(p, b, hq, hkv);
-  const int row0 = blockIdx.x * 32;
+  const int row0 = qt * 32;
   if (row0 >= sv.len_q) return;  // uniform over the workgroup
   const int len_c = (p.flags & ASRATTN_FWD_ZERO_PADDED_ROWS) != 0 ? min(sv.len_q, sv.n_k) : sv.len_q;
 
@@ -183,18 +188,17 @@ __global__ __launch_bounds__(64 * KS, OCC) void fwd_f32mm_kernel(const FwdArgs a
 
   // This wave's sub-tiles ks, ks + KS, ... in register ping-pong: the next
   // sub-tile's operands load while the current one computes.
+  // The loads are unconditional (past the block's last key they read zeros
+  // and are never used): a load under a branch makes the compiler drain
+  // every load at the join, the prefetch included.
   Operands<HD> opa, opb;
-  int sub = ks;
-  if (sub < n_sub) load(opa, sub);
-  while (sub < n_sub) {
-    const int nxt = sub + KS;
-    if (nxt < n_sub) load(opb, nxt);
+  load(opa, ks);
+  for (int sub = ks; sub < n_sub; sub += 2 * KS) {
+    load(opb, sub + KS);
     tile(opa, sub);
-    if (nxt >= n_sub) break;
-    const int nn = nxt + KS;
-    if (nn < n_sub) load(opa, nn);
-    tile(opb, nxt);
-    sub = nn;
+    if (sub + KS >= n_sub) break;
+    load(opa, sub + 2 * KS);
+    tile(opb, sub + KS);
   }
 
   // Merge the key splits through LDS: waves 1..KS-1 store (O^T, max, sum),
@@ -248,9 +252,12 @@ template <int HD, int KS>
 hipError_t launch_ks(const FwdArgs& a, hipStream_t stream) {
   const asrattn_fwd_params& p = a.p;
   const int q_tiles = (p.max_len_q + 31) / 32;
-  // Two waves per SIMD at head_dim 64 (about 210 VGPRs), one at 128.
+  const long long total = (long long)q_tiles * p.heads_q * p.batch;
+  if (total > 0x7fffffffLL) return hipErrorInvalidConfiguration;
+  // Two waves per SIMD at head_dim 64 (about 240 VGPRs), one at 128.
   constexpr int OCC = HD == 64 ? 2 : 1;
-  hipLaunchKernelGGL((fwd_f32mm_kernel<HD, KS, OCC>), dim3(q_tiles, p.heads_q, p.batch), dim3(64 * KS), 0, stream, a);
+  hipLaunchKernelGGL((fwd_f32mm_kernel<HD, KS, OCC>), dim3((unsigned)total), dim3(64 * KS), 0, stream, a, q_tiles,
+                     (int)total);
   return hipGetLastError();
 }
 
@@ -280,16 +287,16 @@ hipError_t launch_hd(const FwdArgs& a, hipStream_t stream) {
 bool fwd_f32mm_supported(const asrattn_fwd_params& p) {
   if (p.dtype != ASRATTN_F32 || p.window > 0) return false;
   if (p.head_dim != 64 && p.head_dim != 128) return false;
-  // K/V addressed with 32-bit byte offsets from the sequence's first key.
-  const long long span_k = ((long long)p.max_len_k + 32) * p.k_token_stride * 4;
-  const long long span_v = ((long long)p.max_len_k + 32) * p.v_token_stride * 4;
+  // K/V addressed with 32-bit byte offsets from the sequence's first key, up
+  // to the prefetch of two rounds of eight 32-key sub-tiles past the last.
+  const long long span_k = ((long long)p.max_len_k + 16 * 32 + 32) * p.k_token_stride * 4;
+  const long long span_v = ((long long)p.max_len_k + 16 * 32 + 32) * p.v_token_stride * 4;
   return span_k < (1LL << 31) && span_v < (1LL << 31) && p.k_token_stride >= p.head_dim &&
          p.v_token_stride >= p.head_dim;
 }
 
 hipError_t launch_fwd_f32mm(const asrattn_fwd_params& p, hipStream_t stream) {
-  if (p.max_len_q > 0x7fffffff - 31 || (long long)p.heads_q > 65535 || (long long)p.batch > 65535)
-    return hipErrorInvalidConfiguration;
+  if (p.max_len_q > 0x7fffffff - 31) return hipErrorInvalidConfiguration;
   FwdArgs a;
   a.p = p;
   a.c = p.scale * kLog2e;
