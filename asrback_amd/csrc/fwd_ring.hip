@@ -368,9 +368,15 @@ __global__ __launch_bounds__(64 * RB * KS * DS, OCC) void fwd_ring_kernel(const 
     const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt), false, false);
     return fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * c;
   };
-  // P^T = 2^(s c - mu) as bf16 MFMA operands; returns the lane's fp32 sum
-  // (a pairwise tree: five dependent adds at 32 values).
+  // P^T = 2^(s c - mu) as bf16 MFMA operands; returns the lane's fp32 sum:
+  // at head_dim 64 the sum of the bf16 P^T operands themselves, two per
+  // v_dot2_f32_bf16 in four chains (Whisper large-v3-turbo's encoder 213.6
+  // -> 208 us per launch; head_dim 128 1-5% slower than fp32 adds), else a
+  // pairwise tree of fp32 adds (five dependent adds at 32 values).
   auto softmax = [&](const f32x16_t* s, float mu, bf16x8_t* pb) {
+    typedef short short2_t __attribute__((ext_vector_type(2)));
+    const short2_t ones = {0x3f80, 0x3f80};  // bf16 1.0
+    float pacc[4] = {0.f, 0.f, 0.f, 0.f};
     float pr[16 * KB];
 #pragma unroll
     for (int t = 0; t < 2 * KB; ++t) {
@@ -382,9 +388,12 @@ __global__ __launch_bounds__(64 * RB * KS * DS, OCC) void fwd_ring_kernel(const 
         pr[8 * t + 2 * i] = p0;
         pr[8 * t + 2 * i + 1] = p1;
         w[i] = pack_bf16x2(p0, p1);
+        if constexpr (HD == 64)
+          pacc[i] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(short2_t, w[i]), ones, pacc[i], false);
       }
       pb[t] = __builtin_bit_cast(bf16x8_t, make_uint4(w[0], w[1], w[2], w[3]));
     }
+    if constexpr (HD == 64) return (pacc[0] + pacc[1]) + (pacc[2] + pacc[3]);
 #pragma unroll
     for (int w = 8 * KB; w >= 1; w /= 2)
 #pragma unroll
