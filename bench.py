@@ -32,7 +32,12 @@ windowed prompt pass.  ``whisper_tiny`` holds Whisper-tiny's float32 lines
 (encoder attention against the fp32 matrix peak, the greedy decoder step's
 attention), ``whole_step`` Whisper-small's whole greedy decoder step with
 the cache write fused into the attention launch against the reference's
-separate writes.
+separate writes.  ``calibration`` times what the card reaches with the
+vendor's libraries in the same run: an 8192^3 GEMM in bf16 and in float32
+(torch.matmul) and a 1 GiB device copy; each bf16 matrix-core line's
+roofline also carries ``frac_of_library_gemm``, its rate over that GEMM's
+(the 2.5 PFLOP/s datasheet peak assumes the 2.4 GHz peak engine clock, which
+the card does not hold under a full bf16 matrix-core load).
 
 ``cpu_baseline`` times the CPU restatement of the reference's attention
 (torch SDPA with the reference's masks, float32, the reference's CPU path)
@@ -937,6 +942,51 @@ class CopyCalibration(Workload):
         return {"workload": self.name, "bytes_read": 1 << 30, "bytes_written": 1 << 30}
 
 
+class GemmCalibration(Workload):
+    """torch.matmul of two (8192, 8192) bf16 matrices (the vendor's tuned
+    GEMM library), four per step: the matrix-core rate a library reaches on
+    this card, beside the datasheet peak, which assumes the 2.4 GHz peak
+    engine clock."""
+
+    name = "gemm-bf16-8192-calibration"
+    unit = "TFLOP/s"
+    bound = "mfma"
+    kernel = "Cijk_"
+    size = 8192
+    per_step = 4
+
+    def __init__(self, torch, attention) -> None:
+        del attention
+        self.torch = torch
+        g = torch.Generator(device="cuda").manual_seed(5)
+        dt = torch.float32 if self.dtype == "f32" else torch.bfloat16
+        self.a, self.b = (torch.randn((self.size, self.size), generator=g, device="cuda", dtype=dt) for _ in range(2))
+        self.c = torch.empty((self.size, self.size), device="cuda", dtype=dt)
+        self.launches = self.per_step
+        self.work_per_step = self.per_step * 2.0 * self.size**3
+
+    def run(self) -> None:
+        for _ in range(self.per_step):
+            self.torch.matmul(self.a, self.b, out=self.c)
+
+    def config(self) -> dict:
+        return {"workload": self.name, "m_n_k": [self.size] * 3, "per_step": self.per_step, "dtype": self.dtype}
+
+
+class GemmCalibrationF32(GemmCalibration):
+    """The same in float32 (no reduced-precision inner products): against the
+    fp32 matrix peak."""
+
+    name = "gemm-f32-8192-calibration"
+    peak = PEAK_FP32_TFLOPS
+    dtype = "f32"
+    per_step = 2
+
+    def __init__(self, torch, attention) -> None:
+        torch.backends.cuda.matmul.allow_tf32 = False
+        super().__init__(torch, attention)
+
+
 _hip = None
 
 
@@ -1375,6 +1425,8 @@ WORKLOADS = {
     "whisper-tiny-step": WhisperTinyDecodeStep,
     "whisper-small-step": WhisperSmallWholeStep,
     "copy": CopyCalibration,
+    "gemm-bf16": GemmCalibration,
+    "gemm-f32": GemmCalibrationF32,
 }
 # The lines of the default run after the headline, by group.
 GROUPS = {
@@ -1382,6 +1434,9 @@ GROUPS = {
     "secondary": ["sensevoice-fsmn", "turbo", "qwen3-prefill", "qwen3-audio", "gemma4-audio", "gemma4-prefill"],
     "whisper_tiny": ["whisper-tiny-encoder", "whisper-tiny-step"],
     "whole_step": ["whisper-small-step"],
+    # What the card reaches with the vendor's libraries: bf16 and fp32 GEMMs
+    # and a 1 GiB device copy (the same card and run as the lines above).
+    "calibration": ["gemm-bf16", "gemm-f32", "copy"],
 }
 
 
@@ -1424,6 +1479,14 @@ def _dispatch_counters(directory: Path, counter: str) -> list[tuple[int, str, fl
         entry = values.setdefault(dispatch, [row["Kernel_Name"], 0.0])
         entry[1] += float(row["Counter_Value"])
     return [(d, k, v) for d, (k, v) in sorted(values.items())]
+
+
+def _dispatch_ns(directory: Path) -> dict[int, int]:
+    """Duration (ns) of each dispatch of a counter run."""
+    spans = {}
+    for row in _csv_rows(directory, "counter_collection.csv"):
+        spans[int(row["Dispatch_Id"])] = int(row["End_Timestamp"]) - int(row["Start_Timestamp"])
+    return spans
 
 
 def profile(out: Path, keys: list[str], steps: int, warmup: int) -> int:
@@ -1521,13 +1584,23 @@ def profile(out: Path, keys: list[str], steps: int, warmup: int) -> int:
             # per dispatch of the dominant kernel (mean over the last two steps).
             _, mdir, mfma_command = child(key, "mfma", ["--pmc", *mfma_counters], 2, 1)
             per = {}
+            spans = _dispatch_ns(mdir)
+            clocks = []
             for name in mfma_counters:
-                vals = [v for _, kernel, v in _dispatch_counters(mdir, name) if cls.kernel in kernel]
-                vals = vals[-2 * cls_launches(plain):] or vals
-                per[name] = statistics.mean(vals) if vals else None
+                rows = [(d, v) for d, kernel, v in _dispatch_counters(mdir, name) if cls.kernel in kernel]
+                rows = rows[-2 * cls_launches(plain):] or rows
+                per[name] = statistics.mean(v for _, v in rows) if rows else None
+                if name == "GRBM_GUI_ACTIVE":
+                    # Busy cycles per XCD over the dispatch's duration: the
+                    # engine clock the kernel ran at.  The counter's window
+                    # is not tight around short dispatches (it reads above
+                    # 2.4 GHz for 20 us ones), so only dispatches of 100 us
+                    # and more give a clock.
+                    clocks = [v / 8 / spans[d] for d, v in rows if spans.get(d, 0) >= 100_000]
             if all(per.get(n) for n in ("SQ_VALU_MFMA_BUSY_CYCLES", "GRBM_GUI_ACTIVE", "SQ_INSTS_MFMA")):
                 cycles = per["GRBM_GUI_ACTIVE"] / 8  # summed over the 8 XCDs
                 mfma_rows[key] = {
+                    "clock_ghz": round(statistics.mean(clocks), 3) if clocks else None,
                     "kernel": short_kernel(kernel_name),
                     "mfma_busy": round(per["SQ_VALU_MFMA_BUSY_CYCLES"] / (cycles * 1024), 4),
                     "coexec_of_busy": round((per["SQ_VALU_MFMA_COEXEC_CYCLES"] or 0) /
@@ -1601,11 +1674,13 @@ def profile(out: Path, keys: list[str], steps: int, warmup: int) -> int:
     ])
     (summaries / "hbm_traffic.md").write_text(text)
     if mfma_rows:
-        rows = ["| Workload | Kernel | µs per launch | MFMA busy | VALU co-executing (share of busy cycles) | "
-                "VALU per MFMA | MFMA per dispatch |", "|---|---|---|---|---|---|---|"]
+        rows = ["| Workload | Kernel | µs per launch | Engine clock GHz | MFMA busy | VALU co-executing (share of busy "
+                "cycles) | VALU per MFMA | MFMA per dispatch |", "|---|---|---|---|---|---|---|---|"]
         for key, e in sorted(mfma_rows.items()):
-            rows.append(f"| {key} | `{e['kernel']}` | {e['us_per_launch']} | {e['mfma_busy']:.1%} | "
-                        f"{e['coexec_of_busy']:.1%} | {e['valu_per_mfma']} | {e['mfma_per_dispatch']} |")
+            clock = e.get("clock_ghz")
+            rows.append(f"| {key} | `{e['kernel']}` | {e['us_per_launch']} | {clock if clock else '—'} | "
+                        f"{e['mfma_busy']:.1%} | {e['coexec_of_busy']:.1%} | {e['valu_per_mfma']} | "
+                        f"{e['mfma_per_dispatch']} |")
         shown = mfma_command or "rocprofv3 --pmc " + " ".join(mfma_counters) + " -- python3 -u bench.py --only <W> ..."
         (summaries / MFMA_FILE.name).write_text("\n".join([
             "# Matrix-core utilisation of the encoder kernels",
@@ -1617,7 +1692,10 @@ def profile(out: Path, keys: list[str], steps: int, warmup: int) -> int:
             "",
             "MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / 8 XCDs x 1024 SIMDs); co-executing = "
             "SQ_VALU_MFMA_COEXEC_CYCLES / SQ_VALU_MFMA_BUSY_CYCLES (matrix cycles during which the same SIMD also "
-            "issued vector ALU work); VALU per MFMA = (SQ_INSTS_VALU - SQ_INSTS_MFMA) / SQ_INSTS_MFMA.  "
+            "issued vector ALU work); VALU per MFMA = (SQ_INSTS_VALU - SQ_INSTS_MFMA) / SQ_INSTS_MFMA; engine "
+            "clock = GRBM_GUI_ACTIVE / 8 / the dispatch's duration, for dispatches of 100 µs and more (the "
+            "datasheet's 2.5 PFLOP/s bf16 and 157.3 TFLOP/s fp32 matrix peaks assume 2.4 GHz); the busy share of "
+            "short dispatches is a lower bound (the counter's window is wider than the dispatch).  "
             f"Kernel sources digest `{digest}`.",
             "",
             *rows,
@@ -1632,7 +1710,8 @@ def profile(out: Path, keys: list[str], steps: int, warmup: int) -> int:
 
 
 def short_kernel(name: str) -> str:
-    """``void ns::(anonymous namespace)::fwd_ring_kernel<...>(...)`` -> ``fwd_ring_kernel``."""
+    """``void ns::(anonymous namespace)::fwd_ring_kernel<...>(...)`` -> ``fwd_ring_kernel``; a library
+    kernel's long generated name (``Cijk_...``) -> its first 24 characters."""
     depth, kept = 0, []
     for ch in name:
         if ch in "<(":
@@ -1641,7 +1720,8 @@ def short_kernel(name: str) -> str:
             kept.append(ch)
         if ch in ">)":
             depth -= 1
-    return "".join(kept).split()[-1].split("::")[-1] if "".join(kept).split() else name
+    short = "".join(kept).split()[-1].split("::")[-1] if "".join(kept).split() else name
+    return short if len(short) <= 48 else short[:24]
 
 
 def cls_launches(result: dict) -> int:
@@ -1720,6 +1800,15 @@ def main() -> int:
                 if key in CPU_BASELINES:
                     result["cpu_baseline"] = cpu_baseline(key, 5.0)
 
+    # Each bf16 matrix-core line against the same run's library GEMM too
+    # (the datasheet peak assumes a clock the card does not hold under a
+    # full matrix-core load).
+    gemm = next((r for r in groups.get("calibration", []) if r["workload"] == GemmCalibration.name), None)
+    if gemm:
+        for result in [head, *(r for lines in groups.values() for r in lines)]:
+            roof = result.get("roofline")
+            if roof and roof["unit"] == "TFLOP/s" and result["dtype"] == "bf16" and result is not gemm:
+                roof["frac_of_library_gemm"] = round(roof["achieved"] / gemm["value"], 4)
     line = {
         "metric": METRIC,
         "value": head["value"],
