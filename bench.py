@@ -1543,6 +1543,8 @@ def profile(out: Path, keys: list[str], steps: int, warmup: int) -> int:
         record = read_traffic()
     workloads = record.get("workloads", {}) if record.get("sources") == digest else {}
     mfma = read_traffic(summaries / MFMA_FILE.name)
+    if mfma.get("sources") != digest:
+        mfma = read_traffic(MFMA_FILE)
     mfma_rows = mfma.get("workloads", {}) if mfma.get("sources") == digest else {}
     mfma_counters = ["SQ_VALU_MFMA_BUSY_CYCLES", "SQ_VALU_MFMA_COEXEC_CYCLES", "SQ_INSTS_MFMA", "SQ_INSTS_VALU",
                      "GRBM_GUI_ACTIVE"]
