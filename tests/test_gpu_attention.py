@@ -120,3 +120,40 @@ def test_gqa_step_golden(golden, ops, device, dtype):
     used = torch.from_numpy(golden["gqa_step_used"]).to(device)
     out = ops.decode(q, k, v, seqused_k=used)
     assert_close(out, golden["gqa_step_out"], KIND[dtype])
+
+
+# --- running-max paths of the matrix-core kernel --------------------------------
+
+
+@pytest.mark.parametrize("hd", [64, 128])
+@pytest.mark.parametrize("pattern", ["growing", "shrinking", "spike", "large"])
+def test_running_max_paths(ops, device, hd, pattern):
+    """Score patterns that drive the matrix-core kernel's running max off its
+    common path, 16 key tiles of 64: row maxima that grow along the keys
+    (rescales after the first tile), that shrink (probabilities far below
+    the first tile's), one late key far above every other for every row
+    (its tile's probabilities overflow the slack: at head_dim 64 the first,
+    max-free exponentiation is thrown away and redone), and scores large
+    throughout.  bf16 against the float32 oracle (torch SDPA)."""
+    say("running max", hd, pattern)
+    g = torch.Generator().manual_seed(70 + hd)
+    batch, heads, length = 2, 3, 1000
+    q, k, v = (torch.randn(batch, heads, length, hd, generator=g) for _ in range(3))
+    ramp = torch.linspace(0.0, 1.0, length)[None, None, :, None]
+    if pattern == "growing":
+        k = k * (1 + 5 * ramp)
+    elif pattern == "shrinking":
+        k = k * (6 - 5 * ramp)
+    elif pattern == "spike":
+        # A direction every query shares, and key 777 along it: its score is
+        # ~18 sqrt(hd) for every row, far above the rest.
+        u = torch.randn(batch, heads, 1, hd, generator=g)
+        q = q + 3 * u
+        k[:, :, 777:778] = 6 * u
+    else:
+        q = q * 6
+    q, k, v = (t.to(torch.bfloat16) for t in (q, k, v))
+    ref = oa.sdpa(q.float(), k.float(), v.float())
+    out = ops.flash(*(t.transpose(1, 2).to(device) for t in (q, k, v)))
+    assert torch.isfinite(out).all()
+    assert_close(out.transpose(1, 2), ref, "bf16")
