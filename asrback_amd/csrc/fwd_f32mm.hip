@@ -266,12 +266,16 @@ hipError_t launch_hd(const FwdArgs& a, hipStream_t stream) {
   const asrattn_fwd_params& p = a.p;
   const long long blocks = (long long)((p.max_len_q + 31) / 32) * p.heads_q * p.batch;
   const int subs = (p.max_len_k + 31) / 32;
-  // Key splits: enough waves for about two per SIMD (1024 SIMDs), and at
-  // least four sub-tiles per split.  At head_dim 128 a wave needs more than
-  // 256 registers, so at most four waves (one per SIMD) per workgroup.
+  // Key splits: as many waves per row block as the CUs hold at once for
+  // all blocks (two per SIMD at head_dim 64; one at 128, where a wave needs
+  // more than 256 registers), and at least two sub-tiles per split.  A
+  // second round of workgroups would run on few CUs: Whisper-tiny's 282 row
+  // blocks take four splits (1128 waves, one round) in 66 us and took 73.8
+  // with eight (2256 waves, two rounds).
   constexpr int kMaxKs = HD == 64 ? 8 : 4;
+  constexpr long long kResidentWaves = HD == 64 ? 2048 : 1024;
   int ks = 1;
-  while (ks < kMaxKs && blocks * ks < 2048 && subs >= 4 * ks) ks *= 2;
+  while (ks < kMaxKs && blocks * 2 * ks <= kResidentWaves && subs >= 4 * ks) ks *= 2;
   switch (ks) {
     case 1: return launch_ks<HD, 1>(a, stream);
     case 2: return launch_ks<HD, 2>(a, stream);

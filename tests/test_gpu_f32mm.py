@@ -40,13 +40,14 @@ def randn(*shape, seed):
 @pytest.mark.parametrize(
     "batch,heads,length,hd",
     [
-        (1, 6, 1500, 64),   # Whisper-tiny encoder layer: 282 row blocks, eight key splits
+        (1, 6, 1500, 64),   # Whisper-tiny encoder layer: 282 row blocks, four key splits
         (1, 1, 1, 64),      # one query, one key
         (2, 3, 33, 64),     # one key split, a partial sub-tile
-        (1, 2, 200, 128),   # head_dim 128, four key splits
-        (4, 2, 95, 128),    # head_dim 128, two key splits
+        (1, 2, 300, 128),   # head_dim 128, four key splits
+        (2, 2, 200, 128),   # head_dim 128, two key splits
+        (4, 2, 95, 128),    # head_dim 128, one key split
         (8, 8, 257, 64),    # two key splits
-        (2, 4, 1000, 64),   # four key splits
+        (2, 4, 1000, 64),   # eight key splits
     ],
 )
 def test_noncausal_matches_oracle_and_valu(ops, device, batch, heads, length, hd):
