@@ -393,12 +393,15 @@ __global__ __launch_bounds__(64 * RB * KS * DS, OCC) void fwd_ring_kernel(const 
       }
       pb[t] = __builtin_bit_cast(bf16x8_t, make_uint4(w[0], w[1], w[2], w[3]));
     }
-    if constexpr (HD == 64) return (pacc[0] + pacc[1]) + (pacc[2] + pacc[3]);
+    if constexpr (HD == 64) {
+      return (pacc[0] + pacc[1]) + (pacc[2] + pacc[3]);
+    } else {
 #pragma unroll
-    for (int w = 8 * KB; w >= 1; w /= 2)
+      for (int w = 8 * KB; w >= 1; w /= 2)
 #pragma unroll
-      for (int i = 0; i < w; ++i) pr[i] += pr[i + w];
-    return pr[0];
+        for (int i = 0; i < w; ++i) pr[i] += pr[i + w];
+      return pr[0];
+    }
   };
   // O^T += V^T . P^T over tile stage stage_idx.  MFMA t covers keys
   // 16 t + 8 (idx / 4) + 4 half + idx % 4.
