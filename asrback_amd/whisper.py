@@ -363,10 +363,13 @@ class GreedyDecoder:
     the decoder step replayed from a HIP graph per (batch bucket, KV bucket).
 
     Restates the decode path of the reference's ``Transcriber`` without its
-    request queue and tokenizer: :meth:`admit` runs the prompts
-    (``_prefill``, ``whisper.py:828-878``), :meth:`advance` runs up to
-    ``EOS_CHECK_INTERVAL`` steps (``:887-915``), :meth:`finished_rows`
-    returns finished rows' tokens (``:917-940``).
+    request queue and tokenizer: :meth:`detect_languages` picks a language
+    token per window (``_detect_languages``, ``whisper.py:976-984``),
+    :meth:`admit` runs the prompts (``_prefill``, ``:828-878``, with the
+    first token's temperatures and the no-speech probability),
+    :meth:`advance` runs up to ``EOS_CHECK_INTERVAL`` steps (``:887-915``),
+    :meth:`finished_rows` returns finished rows' tokens (``:917-940``).
+    Token ids come from the caller (the tokenizer stays outside).
     """
 
     def __init__(
@@ -394,6 +397,8 @@ class GreedyDecoder:
         self.cache = model.allocate_cache(max_batch_size)
         self.staging = model.allocate_cache(max_batch_size)
         self.state = DecodeState.allocate(max_batch_size, max_target, self.device)
+        # Per row: the prompt pass's no-speech probability (admit's no_speech_id).
+        self.no_speech = torch.zeros(max_batch_size, dtype=torch.float32, device=self.device)
         self.workspace = torch.empty(self._workspace_bytes(), dtype=torch.uint8, device=self.device)
         self.rows: dict[int, dict] = {}
         self.graphs: dict[tuple[int, int], CapturedGraph] = {}
@@ -433,13 +438,44 @@ class GreedyDecoder:
         self.state.free(torch.arange(self.max_batch_size, device=self.device))
 
     @torch.inference_mode()
-    def admit(self, encoder_output: Tensor, prefixes: list[list[int]], max_new_tokens: int) -> list[int]:
+    def detect_languages(self, encoder_output: Tensor, start_id: int, language_ids: list[int]) -> list[int]:
+        """The language of each window (``whisper.py:976-984``): one decoder
+        pass over ``start_id`` (<|startoftranscript|>) at position 0 of the
+        staging rows, whose cross-attention takes ``encoder_output``; returns,
+        per window, the index into ``language_ids`` of the largest logit among
+        those tokens.  Position 0 is overwritten by the next :meth:`admit`."""
+        count = len(encoder_output)
+        staging = self.staging.narrow(count)
+        self.model.set_encoder_output(staging, encoder_output)
+        tokens = torch.full((count, 1), start_id, dtype=torch.long, device=self.device)
+        hidden = self.model.decode(tokens, self._positions[:1], staging, length=1)
+        ids = torch.as_tensor(language_ids, dtype=torch.long, device=self.device)
+        return self.model.logits(hidden[:, -1])[:, ids].argmax(dim=-1).tolist()
+
+    @torch.inference_mode()
+    def admit(
+        self,
+        encoder_output: Tensor,
+        prefixes: list[list[int]],
+        max_new_tokens: int,
+        temperatures: Tensor | None = None,
+        sot_index: int | None = None,
+        no_speech_id: int | None = None,
+    ) -> list[int]:
         """Prompt pass for windows that share a prefix length, then move them
-        (with their first token) into free rows; returns their slots."""
+        (with their first token) into free rows; returns their slots.
+
+        ``temperatures`` (one per window, or None for greedy) pick the first
+        token as the reference's ``_choose`` does.  With ``no_speech_id`` the
+        pass also keeps each window's probability of that token after the
+        prompt's <|startoftranscript|> at index ``sot_index``
+        (``whisper.py:848-858``; :meth:`no_speech_probs`)."""
         count = len(prefixes)
         prefix_length = len(prefixes[0])
         if any(len(p) != prefix_length for p in prefixes):
             raise ValueError("admit() takes prompts of one length")
+        if no_speech_id is not None and not (sot_index is not None and 0 <= sot_index < prefix_length):
+            raise ValueError("no_speech_id needs sot_index, the position of <|startoftranscript|> in the prompt")
         slots = [s for s in range(self.max_batch_size) if s not in self.rows][:count]
         if len(slots) < count:
             raise RuntimeError("no free rows")
@@ -447,12 +483,20 @@ class GreedyDecoder:
         self.model.set_encoder_output(staging, encoder_output)
         tokens = to_device(prefixes, self.device)
         hidden = self.model.decode(tokens, self._positions[:prefix_length], staging, length=prefix_length)
-        logits = self.model.logits(hidden[:, -1:]).float()[:, 0]
+        rows = to_device(slots, self.device)
+        if no_speech_id is None:
+            logits = self.model.logits(hidden[:, -1:]).float()[:, 0]
+            self.no_speech[rows] = 0.0
+        else:
+            both = self.model.logits(torch.stack((hidden[:, sot_index], hidden[:, -1]), dim=1)).float()
+            self.no_speech[rows] = both[:, 0].softmax(dim=-1)[:, no_speech_id]
+            logits = both[:, 1]
+        if temperatures is not None:
+            temperatures = torch.as_tensor(temperatures, dtype=torch.float32).to(self.device)
         with attention.workspace(self.workspace):
-            token, logprob = choose(logits, self._first_suppress)
+            token, logprob = choose(logits, self._first_suppress, temperatures)
         available = self.config["max_target_positions"] - prefix_length
         end = prefix_length - 1 + min(max_new_tokens, available)
-        rows = to_device(slots, self.device)
         self.cache.copy_rows(staging, rows, prefix_length)
         state = self.state
         state.tokens[rows] = token[:, None]
@@ -503,6 +547,11 @@ class GreedyDecoder:
         for r in rows:
             r["bound"] = min(r["bound"] + count, r["end"])
         return count
+
+    def no_speech_probs(self, slots: list[int]) -> list[float]:
+        """The no-speech probability :meth:`admit` kept for each slot (0.0
+        when it was given no ``no_speech_id``, as in the reference)."""
+        return self.no_speech[to_device(slots, self.device)].tolist()
 
     @torch.inference_mode()
     def finished_rows(self) -> dict[int, list[int]]:

@@ -116,3 +116,41 @@ def test_bf16_model_decodes(fixture, weights, device):
     (tokens,) = run_rows(dec, model, [mel_for(fixture["seeds"]["mel"])], fixture, device)
     assert len(tokens) == fixture["steps"]
     assert all(0 <= t < fixture["config"]["vocab_size"] for t in tokens)
+
+
+def test_prompt_pass_side_outputs_match_oracle(fixture, weights, device):
+    """The prompt pass's no-speech probability (softmax of the logits after
+    <|startoftranscript|>, whisper.py:848-858) and the detected language
+    (argmax over the language tokens after <|startoftranscript|> alone,
+    :976-984) against the float32 CPU oracle on the same weights, two
+    windows; a temperature of 0 keeps the greedy first token."""
+    print("whisper prompt side outputs", flush=True)
+    torch.set_num_threads(min(8, torch.get_num_threads()))
+    ref = ow.WhisperForConditionalGeneration(fixture["config"]).eval()
+    ref.load_state_dict(weights)
+    model = gpu_model(fixture, weights, device)
+    mel = torch.cat([mel_for(fixture["seeds"]["mel"]), mel_for(77)])
+    languages = list(range(ow.EN, ow.EN + 99))  # the multilingual vocabulary's language tokens
+    no_speech = ow.NO_TIMESTAMPS - 1  # <|nospeech|> there
+    prefix = fixture["prefix"]
+    with torch.inference_mode():
+        enc_ref = ref.model.encoder(mel)
+        cache_ref = ref.allocate_cache(2)
+        ref.set_encoder_output(cache_ref, enc_ref)
+        hid_ref = ref.model.decoder(torch.tensor([prefix] * 2), torch.arange(len(prefix)), cache_ref, len(prefix))
+        probs_ref = ref.logits(hid_ref[:, prefix.index(ow.SOT)]).softmax(dim=-1)[:, no_speech]
+        hid_lang = ref.model.decoder(torch.full((2, 1), ow.SOT), torch.arange(1), cache_ref, 1)
+        lang_logits = ref.logits(hid_lang[:, -1])[:, languages]
+        top2 = lang_logits.topk(2, dim=-1).values
+        assert bool((top2[:, 0] - top2[:, 1] > 1e-3 * top2.abs().max()).all()), "near-tie in the oracle's languages"
+
+        enc = model.model.encoder(mel.to(device))
+        dec = decoder(model, fixture, device, batch=2, graphs=False)
+        detected = dec.detect_languages(enc, ow.SOT, languages)
+        slots = dec.admit(enc, [prefix] * 2, fixture["steps"], temperatures=[0.0, 0.0],
+                          sot_index=prefix.index(ow.SOT), no_speech_id=no_speech)
+        probs = torch.tensor(dec.no_speech_probs(slots))
+        first = dec.state.tokens[slots[0], 0].item()
+    assert detected == lang_logits.argmax(dim=-1).tolist()
+    assert_close(probs, probs_ref, "module", 1e-4)
+    assert first == fixture["tokens"][0]
