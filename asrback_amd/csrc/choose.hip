@@ -131,29 +131,67 @@ __global__ __launch_bounds__(NT) void choose_kernel(const float* logits, int64_t
         sup[k] = __builtin_amdgcn_raw_buffer_load_b8(sr, c, 0, 0);
       }
     }
-    // The round's max and first index of it, then its sum against that max.
-    Best cb{kNegInf, 0x7fffffff, 0.f, 0.f};
+    // Suppressed and out-of-range elements are -inf.
 #pragma unroll
     for (int k = 0; k < kChunk; ++k) {
-      const int64_t c = c0 + tid + k * NT;
+      const bool in = c0 + tid + k * NT < g1;
 #pragma unroll
-      for (int q = 0; q < Q; ++q) {
-        const bool live = c < g1 && ((sup[k] >> (8 * q)) & 0xffu) == 0;
-        xs[k][q] = live ? xs[k][q] : kNegInf;
-        const int i = (int)(c * Q + q);
-        if (beats(xs[k][q], i, cb.m, cb.idx)) {
-          cb.m = xs[k][q];
-          cb.idx = i;
-        }
-      }
+      for (int q = 0; q < Q; ++q)
+        xs[k][q] = in && ((sup[k] >> (8 * q)) & 0xffu) == 0 ? xs[k][q] : kNegInf;
     }
-    if (cb.m != cb.m) {
-      cb.sum = cb.m;  // a NaN is the round's max, and its sum is NaN
-    } else {
+    // The round's max, the first index of it and its sum against it.  Fast
+    // path: a plain max (which skips NaN), the first element equal to it,
+    // then the sum, which a NaN element or an infinite max turns into NaN;
+    // such a round, or a round whose max is -inf but which holds a NaN, is
+    // redone under the exact rule (beats).  A round of nothing but -inf adds
+    // nothing.  (Qwen3's (64, 151936) logits: 19.9 -> 16.6 us per choice
+    // against the exact rule alone.)
+    Best cb{kNegInf, 0x7fffffff, 0.f, 0.f};
+    float m = xs[0][0];
+#pragma unroll
+    for (int k = 0; k < kChunk; ++k)
+#pragma unroll
+      for (int q = 0; q < Q; ++q) m = fmaxf(m, xs[k][q]);
+    bool exact = false;
+    if (m == kNegInf) {
 #pragma unroll
       for (int k = 0; k < kChunk; ++k)
 #pragma unroll
-        for (int q = 0; q < Q; ++q) cb.sum += exp_diff(xs[k][q], cb.m);
+        for (int q = 0; q < Q; ++q) exact |= xs[k][q] != xs[k][q];
+    } else {
+      int idx = 0x7fffffff;
+#pragma unroll
+      for (int k = kChunk - 1; k >= 0; --k)
+#pragma unroll
+        for (int q = Q - 1; q >= 0; --q) idx = xs[k][q] == m ? (int)((c0 + tid + k * NT) * Q + q) : idx;
+      float sum = 0.f;  // the exact rule's terms: exp_diff, whose -inf case gives 0 here
+#pragma unroll
+      for (int k = 0; k < kChunk; ++k)
+#pragma unroll
+        for (int q = 0; q < Q; ++q) sum += fast_exp2((xs[k][q] - m) * kLog2e);
+      cb = Best{m, idx, sum, 0.f};
+      exact = sum != sum;
+    }
+    if (exact) {
+      cb = Best{kNegInf, 0x7fffffff, 0.f, 0.f};
+#pragma unroll
+      for (int k = 0; k < kChunk; ++k)
+#pragma unroll
+        for (int q = 0; q < Q; ++q) {
+          const int i = (int)((c0 + tid + k * NT) * Q + q);
+          if (beats(xs[k][q], i, cb.m, cb.idx)) {
+            cb.m = xs[k][q];
+            cb.idx = i;
+          }
+        }
+      if (cb.m != cb.m) {
+        cb.sum = cb.m;  // a NaN is the round's max, and its sum is NaN
+      } else {
+#pragma unroll
+        for (int k = 0; k < kChunk; ++k)
+#pragma unroll
+          for (int q = 0; q < Q; ++q) cb.sum += exp_diff(xs[k][q], cb.m);
+      }
     }
     s = merge(s, cb);
   }

@@ -770,17 +770,23 @@ def _torch_choice(logits: torch.Tensor, suppress: torch.Tensor | None):
 def test_greedy_choice_matches_torch(ops, device, vocab):
     """argmax + log_softmax at it in one pass (whisper.py:962-974,
     qwen3_asr.py:1200-1210) against torch on the CPU: tokens exact,
-    log-probabilities to 1e-5; rows with ties, a suppress mask, NaN and
-    all -inf rows; odd vocabularies take the element-wise path."""
+    log-probabilities to 1e-5; rows with ties, a suppress mask, NaN, +inf
+    and all -inf rows (and a NaN among -inf values only, which a plain max
+    skips); odd vocabularies take the element-wise path."""
     say("greedy choice", vocab)
     g = torch.Generator().manual_seed(80 + vocab % 97)
-    logits = torch.randn(9, vocab, generator=g) * 4
+    logits = torch.randn(12, vocab, generator=g) * 4
     logits[1, 7] = logits[1, vocab - 3] = logits[1].max() + 1.0  # tie: first index wins
     logits[2, :] = 0.5  # all equal
     logits[3, 5] = float("nan")
     logits[3, 9] = float("nan")
     logits[4, :] = float("-inf")
     logits[5, : vocab // 2] = float("-inf")
+    logits[9, :] = float("-inf")
+    logits[9, vocab // 3] = float("nan")  # the only non -inf value
+    logits[10, 11] = logits[10, vocab - 5] = float("inf")  # +inf twice: the first wins
+    logits[11, : vocab // 2] = float("-inf")
+    logits[11, vocab // 4] = float("nan")  # inside the -inf half
     suppress = torch.zeros(vocab, dtype=torch.bool)
     suppress[torch.randperm(vocab, generator=g)[: vocab // 10]] = True
     suppress[int(logits[6].argmax())] = True  # the row's max is suppressed
