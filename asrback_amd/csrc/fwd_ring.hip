@@ -84,7 +84,7 @@ constexpr int kRankMinKeys = 128;
 // Launch id -> (sequence, query head, query tile).  Dispatch hands ids out
 // in order as workgroup slots free up, round-robin over the 8 XCDs.  With
 // per-sequence key counts (ragged batches of at most 64 sequences, some
-// longer than kRankMinKeys) the
+// longer than kRankMinKeys, none of 2^25 keys or more) the
 // (sequence, kv head) units are taken in decreasing key count -- the
 // longest work starts first and short units fill in behind it -- and unit U
 // goes to XCD U % 8 with all its items consecutive there (every query head
@@ -96,7 +96,8 @@ constexpr int kRankMinKeys = 128;
 __device__ __forceinline__ void work_item(const asrattn_fwd_params& p, int q_tiles, int total, int id, int& b,
                                           int& hq, int& qt) {
   const bool ragged = p.seqused_k != nullptr || p.cu_seqlens_k != nullptr;
-  if (ragged && p.max_len_k > kRankMinKeys && p.batch <= 64 && (p.batch * p.heads_kv) % 8 == 0) {
+  if (ragged && p.max_len_k > kRankMinKeys && p.max_len_k < (1 << 25) && p.batch <= 64 &&
+      (p.batch * p.heads_kv) % 8 == 0) {
     const int group = p.heads_q / p.heads_kv;
     const int per_unit = group * q_tiles;
     const int per = total / 8, half = per / 2;

@@ -78,19 +78,20 @@ __device__ __forceinline__ int sequence_keys(const asrattn_fwd_params& p, int b)
 }
 
 // Rank of lane's key count n among lanes 0 .. N - 1 (decreasing count, ties
-// in lane order); lanes past the batch hold -1, below every count.  Unrolled
-// with a constant bound, so the compiler overlaps each lane read with the
-// compares of the one before (a loop to the batch size waited on every
-// read: SenseVoice's 32 sequences 20.1 -> 19.8 us per launch, with the FSMN
-// memory 27.6 -> 26.5).
+// in lane order); lanes past the batch hold -1, below every count.  Each
+// lane's (count, lane) pair is one unique 32-bit key, (n << 6) | (63 - lane)
+// (n < 2^25, which the caller checks), so a step is a lane read and one
+// compare.  Unrolled with a constant bound, so the compiler overlaps each
+// lane read with the compare of the one before (a loop to the batch size
+// waited on every read: SenseVoice's 32 sequences 20.1 -> 19.8 us per
+// launch, with the FSMN memory 27.6 -> 26.5; the single-compare key a
+// further 0-3%).
 template <int N>
 __device__ __forceinline__ int count_rank(int n, int lane) {
+  const uint32_t key = n < 0 ? 0u : ((uint32_t)n << 6) | (uint32_t)(63 - lane);
   int rank = 0;
 #pragma unroll
-  for (int j = 0; j < N; ++j) {
-    const int nj = __builtin_amdgcn_readlane(n, j);
-    rank += (nj > n || (nj == n && j < lane)) ? 1 : 0;
-  }
+  for (int j = 0; j < N; ++j) rank += (uint32_t)__builtin_amdgcn_readlane((int)key, j) > key ? 1 : 0;
   return rank;
 }
 
