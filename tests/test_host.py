@@ -224,3 +224,23 @@ def test_whisper_choose_samples_where_temperature_is_positive():
     scaled = masked / temperatures.clamp(min=1e-6)[:, None]
     sampled = torch.multinomial(torch.softmax(scaled, dim=-1), 1).squeeze(1)
     assert torch.equal(token, torch.where(temperatures > 0, sampled, masked.argmax(dim=-1)))
+
+
+def test_whisper_admit_checks_the_no_speech_arguments():
+    """admit() with a no_speech_id needs the prompt position of
+    <|startoftranscript|> (whisper.py:848-858); the check comes before any
+    device work, so a wrong call fails on any machine."""
+    import json
+
+    from conftest import GOLDEN
+
+    from asrback_amd import whisper as aw
+
+    config = json.loads((GOLDEN / "whisper_tiny_greedy.json").read_text())["config"]
+    model = aw.WhisperForConditionalGeneration(config).eval()
+    suppress = torch.zeros(config["vocab_size"], dtype=torch.bool)
+    dec = aw.GreedyDecoder(model, 2, suppress, suppress, config["eos_token_id"], graphs=False)
+    encoded = torch.zeros(1, config["max_source_positions"], config["d_model"])
+    for sot_index in (None, 4, -1):
+        with pytest.raises(ValueError, match="sot_index"):
+            dec.admit(encoded, [[1, 2, 3, 4]], 8, no_speech_id=5, sot_index=sot_index)
