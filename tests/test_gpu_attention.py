@@ -157,3 +157,24 @@ def test_running_max_paths(ops, device, hd, pattern):
     out = ops.flash(*(t.transpose(1, 2).to(device) for t in (q, k, v)))
     assert torch.isfinite(out).all()
     assert_close(out.transpose(1, 2), ref, "bf16")
+
+
+@pytest.mark.parametrize("batch", [5, 12, 24, 40, 64, 65])
+@pytest.mark.parametrize("hd", [64, 128])
+def test_ragged_work_order_batches(ops, device, batch, hd):
+    """Ragged batches of every size class of the longest-first work order
+    (the ranking's 8-, 16-, 32- and 64-sequence bounds; 65 sequences are
+    not ranked), key counts 1-300 with ties, bf16 against the oracle."""
+    say("ragged work order", batch, hd)
+    rng = np.random.default_rng(200 + batch)
+    lengths = rng.integers(1, 301, size=batch).astype(np.int32)
+    lengths[: batch // 3] = lengths[batch // 3]  # ties: index order decides
+    length = int(lengths.max())
+    heads = 8
+    g = torch.Generator().manual_seed(210 + batch + hd)
+    q, k, v = (torch.randn(batch, length, heads, hd, generator=g).to(torch.bfloat16) for _ in range(3))
+    used = torch.from_numpy(lengths)
+    ref = oa.sdpa(*(t.float().transpose(1, 2) for t in (q, k, v)),
+                  attn_mask=oa.key_padding_mask(used, length)[:, None, None, :]).transpose(1, 2)
+    out = ops.flash(q.to(device), k.to(device), v.to(device), seqused_k=used.to(device))
+    assert_close(out.float().cpu(), ref, "bf16")
