@@ -1,7 +1,16 @@
 #!/usr/bin/env python3
 """Throughput of the asrback attention hot path on one MI355X.
 
-Prints one JSON line.  The headline workload is SenseVoiceSmall's SAN-M
+Prints progress lines, then one JSON line holding every line below in full
+(``"detail": true``), then the result line, last and compact: the headline
+with its roofline and CPU baseline, and ``configs``, one entry per
+benchmark configuration (1 Whisper-tiny fp32 encoder and decoder step, 2
+SenseVoice, 3 Whisper-small decoder step, 4 Whisper large-v3-turbo encoder,
+5 Qwen3-ASR-1.7B decode) with its rate, median ms per step, steps timed,
+work per step, roofline fraction, HBM traffic per launch and CPU baseline.
+Workloads that advance positions through a fixed schedule (Qwen3's 128
+decode steps, Whisper-tiny's 32) time the whole schedule whatever --steps
+says.  The headline workload is SenseVoiceSmall's SAN-M
 encoder self-attention in bf16 (4 heads x 128, 70 layers, batch 32 with
 ragged lengths of 104-504 frames and key padding): a step is the attention of
 all 70 layers over one batch, q/k/v read in place from per-layer fused
@@ -20,15 +29,16 @@ a (28, 64, 1024, 8, 128) cache, 128 steps; also over a paged cache of
 1500 frames), in algorithmic HBM GB/s (K and V of the keys each row uses,
 plus q and o), and the Qwen3 step with its prologue (per-head RMSNorm and
 rotary embedding of q and k, the cache write) fused into the decode launch,
-timed beside the unfused sequence of ops, the greedy token choice over
-Qwen3's (64, 151936) logits in one pass, and Gemma 4's decoder step (sliding
-layers over a 512-key window at head_dim 256, full layers at 512).
-``secondary`` adds the SenseVoice attention with its FSMN memory fused into
-the same launch (timed beside the reference's ops for both outputs), Whisper
-large-v3-turbo's encoder attention (20 heads x 64, 1500 frames, batch 16, 32
-layers), Qwen3's causal grouped-query prompt pass and its audio encoder's
-windowed attention, Gemma 4's blocked local audio attention and Gemma 4's
-windowed prompt pass.  ``whisper_tiny`` holds Whisper-tiny's float32 lines
+timed beside the unfused sequence of ops, and the greedy token choice over
+Qwen3's (64, 151936) logits in one pass.  ``secondary`` adds the SenseVoice
+attention with its FSMN memory fused into the same launch (timed beside the
+reference's ops for both outputs), Whisper large-v3-turbo's encoder
+attention (20 heads x 64, 1500 frames, batch 16, 32 layers), and Qwen3's
+causal grouped-query prompt pass and its audio encoder's windowed
+attention.  Gemma 4's lines (its decoder step: sliding layers over a
+512-key window at head_dim 256, full layers at 512; its blocked local audio
+attention; its windowed prompt pass) run with --only gemma4-decode,
+gemma4-audio, gemma4-prefill.  ``whisper_tiny`` holds Whisper-tiny's float32 lines
 (encoder attention against the fp32 matrix peak, the greedy decoder step's
 attention), ``whole_step`` Whisper-small's whole greedy decoder step with
 the cache write fused into the attention launch against the reference's
@@ -80,7 +90,9 @@ METRIC = "attn TFLOP/s (encoder) & HBM GB/s (decode step), % of MI355X roofline"
 
 
 def log(*args) -> None:
-    print(*args, file=sys.stderr, flush=True)
+    """Progress, on stdout before the result lines (so that the last line
+    printed is the result)."""
+    print(*args, flush=True)
 
 
 class Workload:
@@ -147,10 +159,10 @@ class SenseVoiceEncoder(Workload):
             "heads": self.heads,
             "head_dim": self.head_dim,
             "layers": self.layers,
-            "frames": "U{100..500} + 4 queries, key padding",
-            "lengths_mean": float(self.lengths_host.mean()),
+            "frames": "L=U{100..500}+4, key padding",
+            "lengths_mean": round(float(self.lengths_host.mean()), 1),
             "max_length": self.length,
-            "padded_rows": "zeros (not computed), as SANMAttention runs it",
+            "padded_rows": "zeroed, not computed",
         }
 
 
@@ -699,12 +711,12 @@ class GreedyChoice(Workload):
 
     def __init__(self, torch, attention, seed: int = 5) -> None:
         self.torch = torch
-        self.rows, self.vocab, self.steps = 64, 151936, 8
+        self.rows, self.vocab, self.choices = 64, 151936, 8
         g = torch.Generator(device="cuda").manual_seed(seed)
-        self.logits = [torch.randn((self.rows, self.vocab), generator=g, device="cuda") * 4 for _ in range(self.steps)]
+        self.logits = [torch.randn((self.rows, self.vocab), generator=g, device="cuda") * 4 for _ in range(self.choices)]
         self.attention = attention
-        self.launches = self.steps
-        self.work_per_step = float(self.steps * (self.rows * self.vocab * 4 + self.rows * 12))
+        self.launches = self.choices
+        self.work_per_step = float(self.choices * (self.rows * self.vocab * 4 + self.rows * 12))
         self.unfused = False
 
     def run(self) -> None:
@@ -718,7 +730,7 @@ class GreedyChoice(Workload):
 
     def config(self) -> dict:
         return {"workload": self.name, "rows": self.rows, "vocab": self.vocab, "dtype": "float32 logits",
-                "choices_per_step": self.steps}
+                "choices_per_step": self.choices}
 
 
 class WhisperSmallDecoderStep(Workload):
@@ -1143,8 +1155,10 @@ def timed_against(torch, workload: Workload, steps: int, warmup: int, result: di
 
 def measure(torch, workload: Workload, key: str, steps: int, warmup: int, compare: bool = True) -> dict:
     if hasattr(workload, "steps"):
-        # Workloads that advance positions: at most their step count is timed.
-        steps = min(steps, workload.steps)
+        # Workloads that advance positions through a fixed schedule (Qwen3's
+        # 128 decode steps, Whisper's 32) time the whole schedule, whatever
+        # --steps asks, so that the bytes per step are the schedule's mean.
+        steps = workload.steps
         warmup = min(warmup, workload.steps)
     timing = time_graph(torch, workload, steps, warmup)
     ms = timing["median"]
@@ -1214,7 +1228,7 @@ def _cpu_timed(fn, work: float, scale: float, unit: str, sample: str, budget_s: 
         "unit": unit,
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": f"{sample}; median of {len(times)} runs ({median * 1e3:.1f} ms each); {_cpu_model()}",
+        "sample": f"{sample}; median of {len(times)} runs of {median * 1e3:.1f} ms; {_cpu_model()}",
         "seconds": round(sum(times), 2),
     }
 
@@ -1233,7 +1247,7 @@ def cpu_sensevoice(budget_s: float) -> dict:
     mask = oa.key_padding_mask(lengths, length)
     work = float(sum(4 * int(n) ** 2 * 512 for n in lengths))
     return _cpu_timed(lambda: oa.sensevoice_attention(qkv, 4, mask), work, 1e12, "TFLOP/s",
-                      f"one layer over the headline batch (B=32, lengths {int(lengths.min())}-{length}), float32",
+                      f"one layer, B=32, lengths {int(lengths.min())}-{length}, float32",
                       budget_s)
 
 
@@ -1428,16 +1442,37 @@ WORKLOADS = {
     "gemm-bf16": GemmCalibration,
     "gemm-f32": GemmCalibrationF32,
 }
-# The lines of the default run after the headline, by group.
+# The lines of the default run after the headline, by group.  Gemma 4's
+# lines (gemma4-decode, gemma4-audio, gemma4-prefill) run with --only.
 GROUPS = {
-    "decode": ["qwen3", "qwen3-paged", "qwen3-fused", "whisper-small", "choice", "gemma4-decode"],
-    "secondary": ["sensevoice-fsmn", "turbo", "qwen3-prefill", "qwen3-audio", "gemma4-audio", "gemma4-prefill"],
+    "decode": ["qwen3", "qwen3-paged", "qwen3-fused", "whisper-small", "choice"],
+    "secondary": ["sensevoice-fsmn", "turbo", "qwen3-prefill", "qwen3-audio"],
     "whisper_tiny": ["whisper-tiny-encoder", "whisper-tiny-step"],
     "whole_step": ["whisper-small-step"],
     # What the card reaches with the vendor's libraries: bf16 and fp32 GEMMs
     # and a 1 GiB device copy (the same card and run as the lines above).
     "calibration": ["gemm-bf16", "gemm-f32", "copy"],
 }
+# The five benchmark configurations and the line that measures each: 1
+# Whisper-tiny fp32 (encoder attention and the greedy step's attention), 2
+# SenseVoice (the headline), 3 Whisper-small's decoder step, 4 Whisper
+# large-v3-turbo's encoder, 5 Qwen3-ASR-1.7B's decode.
+CONFIG_LINES = [(1, "whisper-tiny-encoder"), (1, "whisper-tiny-step"), (2, "sensevoice"), (3, "whisper-small"),
+                (4, "turbo"), (5, "qwen3")]
+
+
+def config_entry(cfg: int, key: str, result: dict) -> dict:
+    """One configuration's figures in the final line, compact: its line (the
+    --only name of its workload), rate, median ms per step, steps timed,
+    algorithmic work per step (flop or bytes), roofline fraction, HBM
+    traffic per launch and CPU baseline rate (same unit; host cores as the
+    headline's)."""
+    roof = result.get("roofline") or {}
+    cpu = result.get("cpu_baseline") or {}
+    work = result["work_per_launch"] * (roof.get("launches_per_step") or 1)
+    return {"cfg": cfg, "line": key, "value": result["value"], "unit": result["unit"],
+            "ms_per_step": result["ms_per_step"], "steps": result["steps_timed"], "work_per_step": f"{work:.3g}",
+            "frac": roof.get("frac"), "traffic": roof.get("traffic"), "cpu": cpu.get("value")}
 
 
 def _run_child(cmd: list[str], limit: float) -> tuple[int, str, str]:
@@ -1774,10 +1809,16 @@ def main() -> int:
         shape_sweep(torch, attention)
         return 0
 
+    # One caller-owned workspace (zeroed: its first 64 KB are the decode
+    # kernel's arrival counters) for every workload's decode and choice
+    # partials, as the decoders hold theirs: a fixed address in the graphs.
+    workspace = torch.zeros(64 << 20, dtype=torch.uint8, device="cuda")
+
     def run(key: str, compare: bool = True) -> dict:
         log(f"bench: {key}")
-        workload = WORKLOADS[key](torch, attention)
-        result = measure(torch, workload, key, args.steps, args.warmup, compare)
+        with attention.workspace(workspace):
+            workload = WORKLOADS[key](torch, attention)
+            result = measure(torch, workload, key, args.steps, args.warmup, compare)
         del workload
         torch.cuda.empty_cache()
         return result
@@ -1796,6 +1837,7 @@ def main() -> int:
     if not args.no_cpu_baseline:
         log("bench: cpu baselines")
         baseline = cpu_baseline("sensevoice", 8.0)
+        head["cpu_baseline"] = baseline
         for lines in groups.values():
             for result in lines:
                 key = next(k for k, cls in WORKLOADS.items() if cls.name == result["workload"])
@@ -1811,6 +1853,14 @@ def main() -> int:
             roof = result.get("roofline")
             if roof and roof["unit"] == "TFLOP/s" and result["dtype"] == "bf16" and result is not gemm:
                 roof["frac_of_library_gemm"] = round(roof["achieved"] / gemm["value"], 4)
+    by_key = {"sensevoice": head}
+    for lines in groups.values():
+        for result in lines:
+            by_key[next(k for k, cls in WORKLOADS.items() if cls.name == result["workload"])] = result
+    # Every line, in full, on one line of its own; the result line follows it.
+    print(json.dumps({"detail": True, "headline": head, **groups}), flush=True)
+    roof = {k: v for k, v in head["roofline"].items()
+            if k not in ("launches_per_step", "flop_per_byte", "ceiling", "frac_of_ceiling")}
     line = {
         "metric": METRIC,
         "value": head["value"],
@@ -1823,14 +1873,13 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (seeded N(0,1) q/k/v and caches, resident in HBM)",
+        "data": "synthetic (seeded N(0,1) inputs resident in HBM)",
         "config": head["config"],
-        "roofline": head["roofline"],
-        "cpu_baseline": baseline,
-        "ms_per_step_mean": head["ms_per_step_mean"],
-        **groups,
+        "roofline": roof,
+        "cpu_baseline": None if baseline is None else {k: v for k, v in baseline.items() if k != "seconds"},
+        "configs": [config_entry(cfg, key, by_key[key]) for cfg, key in CONFIG_LINES if key in by_key],
     }
-    print(json.dumps(line), flush=True)
+    print(json.dumps(line, separators=(",", ":")), flush=True)
     return 0
 
 

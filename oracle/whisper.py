@@ -31,11 +31,15 @@ WHISPER_TINY = {
     "max_target_positions": 448,
     "vocab_size": 51865,
     "eos_token_id": 50257,
+    # The multilingual checkpoints' lists (WhisperConfig's own default for
+    # begin_suppress_tokens, (220, 50256), is the English-only tokenizer's
+    # end token); no configured suppressions beyond the timestamp tokens.
+    "suppress_tokens": [],
+    "begin_suppress_tokens": [220, 50257],
 }
 # Multilingual tokenizer ids: <|startoftranscript|>, <|en|>, <|transcribe|>,
 # <|notimestamps|>.
 SOT, EN, TRANSCRIBE, NO_TIMESTAMPS = 50258, 50259, 50359, 50363
-BEGIN_SUPPRESS = (220, 50257)
 
 
 class MultiHeadAttention(nn.Module):
@@ -193,12 +197,16 @@ class WhisperForConditionalGeneration(nn.Module):
 
 
 def suppress_masks(config: dict) -> tuple[Tensor, Tensor]:
-    """Tokens never sampled: every timestamp token (``whisper.py:536-544``);
-    the first step also suppresses the begin tokens."""
+    """Tokens never sampled (``whisper.py:536-544``): the config's
+    ``suppress_tokens`` and every timestamp token (ids above
+    <|notimestamps|>); the first step also suppresses the config's
+    ``begin_suppress_tokens``.  A config without the lists suppresses only
+    the timestamps, as the reference's ``config.get(..., [])`` does."""
     suppress = torch.zeros(config["vocab_size"], dtype=torch.bool)
+    suppress[list(config.get("suppress_tokens", []))] = True
     suppress[NO_TIMESTAMPS + 1 :] = True
     first = suppress.clone()
-    first[list(BEGIN_SUPPRESS)] = True
+    first[list(config.get("begin_suppress_tokens", []))] = True
     return suppress, first
 
 

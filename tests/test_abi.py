@@ -345,3 +345,32 @@ def test_choose_workspace_size_and_errors(lib):
     assert status == _lib.ERR_WORKSPACE
     assert b"workspace" in lib.asrattn_last_error()
     assert lib.asrattn_choose(fake, 64, 151936, 151936, None, fake, fake, None, 16, None) == _lib.ERR_INVALID
+
+
+def test_zero_padded_rows_needs_the_padded_noncausal_layout(lib):
+    """ASRATTN_FWD_ZERO_PADDED_ROWS is refused with cu_seqlens, with causal
+    attention and without seqused_k, before any device call (the pointers
+    are stand-ins, never dereferenced)."""
+    from asrback_amd import _lib
+
+    def params():
+        f = _lib.FwdParams()
+        f.batch, f.heads_q, f.heads_kv, f.head_dim = 2, 4, 4, 128
+        f.max_len_q = f.max_len_k = 300
+        f.dtype, f.scale, f.flags = _lib.BF16, 128**-0.5, 2  # ASRATTN_FWD_ZERO_PADDED_ROWS
+        f.q = f.k = f.v = f.out = 4096
+        f.seqused_k = 64
+        return f
+
+    f = params()
+    f.cu_seqlens_q = f.cu_seqlens_k = 128
+    assert lib.asrattn_fwd(ctypes.byref(f), None) == _lib.ERR_INVALID
+    assert b"ZERO_PADDED_ROWS" in lib.asrattn_last_error()
+    f = params()
+    f.causal = 1
+    assert lib.asrattn_fwd(ctypes.byref(f), None) == _lib.ERR_INVALID
+    assert b"ZERO_PADDED_ROWS" in lib.asrattn_last_error()
+    f = params()
+    f.seqused_k = None
+    assert lib.asrattn_fwd(ctypes.byref(f), None) == _lib.ERR_INVALID
+    assert b"ZERO_PADDED_ROWS" in lib.asrattn_last_error()

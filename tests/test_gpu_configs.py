@@ -40,12 +40,16 @@ def randn(*shape, seed, dtype=torch.float32):
 # --- encoder self-attention ----------------------------------------------------
 
 
+@pytest.mark.parametrize("zero_padded", [False, True])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_sensevoice_ragged_batch(ops, device, dtype):
+def test_sensevoice_ragged_batch(ops, device, dtype, zero_padded):
     """SenseVoice SAN-M: B=32, 4 x 128, lengths 4 + U{100..500}, key padding
     through seqused_k on views of the fused (B, L, 1536) projection
-    (sensevoice.py:97, :110-133)."""
-    say("sensevoice ragged", dtype)
+    (sensevoice.py:97, :110-133).  With ``zero_padded_rows`` -- the launch
+    the headline line times (bench.py's SenseVoice workload, as
+    SANMAttention runs it) -- the valid rows are checked against the oracle
+    and every padded row must be exactly zero."""
+    say("sensevoice ragged", dtype, "zero_padded", zero_padded)
     rng = np.random.default_rng(11)
     lengths = torch.from_numpy((rng.integers(100, 501, size=32) + 4).astype(np.int32))
     length = int(lengths.max())
@@ -53,8 +57,14 @@ def test_sensevoice_ragged_batch(ops, device, dtype):
     ref = oa.sensevoice_attention(fused.float(), 4, oa.key_padding_mask(lengths, length))
     x = fused.to(device)
     q, k, v = (t.view(32, length, 4, 128) for t in x.split(512, dim=-1))
-    out = ops.flash(q, k, v, seqused_k=lengths.to(device))
-    assert_close(out.reshape(32, length, 512), ref, KIND[dtype])
+    out = ops.flash(q, k, v, seqused_k=lengths.to(device), zero_padded_rows=zero_padded).reshape(32, length, 512)
+    if not zero_padded:
+        assert_close(out, ref, KIND[dtype])
+        return
+    valid = torch.arange(length)[None, :] < lengths[:, None]  # (32, length)
+    out = out.float().cpu()
+    assert_close(out[valid], ref[valid], KIND[dtype], label="valid rows")
+    assert not out[~valid].any(), "padded rows must be exactly zero"
 
 
 def test_sensevoice_unmasked_equals_masked_full_length(ops, device):

@@ -154,3 +154,32 @@ def test_prompt_pass_side_outputs_match_oracle(fixture, weights, device):
     assert detected == lang_logits.argmax(dim=-1).tolist()
     assert_close(probs, probs_ref, "module", 1e-4)
     assert first == fixture["tokens"][0]
+
+
+def test_choose_samples_only_where_temperature_is_positive(device):
+    """whisper.py:962-974 with temperatures (0, 0.8): the product's choose
+    runs the reference's ops for the whole batch -- the zero-temperature
+    row takes the greedy token (the fused greedy pass's choice), the other
+    samples under a seeded generator, and each row's log-probability is the
+    unscaled log_softmax at its token, suppressed tokens included as -inf."""
+    from asrback_amd import attention
+    from asrback_amd import whisper as aw
+
+    vocab = ow.WHISPER_TINY["vocab_size"]
+    g = torch.Generator().manual_seed(31)
+    logits = (torch.randn(2, vocab, generator=g) * 3).to(device)
+    suppress, _ = ow.suppress_masks(ow.WHISPER_TINY)
+    suppress = suppress.to(device)
+    greedy_token, greedy_logprob = attention.greedy_choice(logits.clone(), suppress)
+    reference = torch.log_softmax(logits.masked_fill(suppress, float("-inf")), dim=-1).cpu()
+    temperatures = torch.tensor([0.0, 0.8], device=device)
+    torch.manual_seed(32)
+    token, logprob = aw.choose(logits.clone(), suppress, temperatures)
+    token, logprob = token.cpu(), logprob.cpu()
+    assert token[0] == greedy_token[0].cpu()
+    assert torch.allclose(logprob[0], greedy_logprob[0].cpu(), rtol=1e-5, atol=1e-5)
+    assert not suppress[token[1]]
+    assert torch.allclose(logprob, reference.gather(1, token[:, None]).squeeze(1), rtol=1e-5, atol=1e-5)
+    torch.manual_seed(32)
+    again, _ = aw.choose(logits.clone(), suppress, temperatures)
+    assert torch.equal(again.cpu(), token)  # the seeded draw repeats

@@ -310,3 +310,38 @@ def test_gemma_relative_positions_and_window():
         u, c = divmod(i, 12)
         keys = [u * 12 - 12 + t for t in range(24) if bool(allowed[u, c, t])]
         assert keys == list(range(max(0, i - 11), i + 1))
+
+
+@pytest.mark.parametrize("source", ["oracle", "asrback_amd"])
+def test_sinusoidal_positions_closed_form(source):
+    """SenseVoice's position encoding (sensevoice.py:166-174) against values
+    the definition fixes, at the model's depth 512: column i < 256 of
+    position p (rows are positions 1, 2, ...) is sin(p * 10000^(-i/255)),
+    column 256 + i its cosine.  Pinned: row 0 is position 1 (not 0), column
+    0 is sin(p) (frequency 1), the last frequency is exactly 1e-4 (the
+    exponent's denominator is depth/2 - 1), sines come before cosines in
+    two halves (not interleaved), and sin^2 + cos^2 = 1."""
+    if source == "oracle":
+        from oracle.sensevoice import sinusoidal_positions as encode
+
+        table = encode(600, 512).double()
+    else:
+        from asrback_amd.sensevoice import sinusoidal_positions as encode
+
+        table = encode(600, 512, torch.device("cpu")).double()
+    assert table.shape == (600, 512)
+    p = torch.arange(1, 601, dtype=torch.float64)
+    # float32 phases up to 600 rad carry ~4e-5 rad of rounding.
+    assert torch.allclose(table[0, :256], torch.sin(torch.tensor([10000.0 ** (-i / 255) for i in range(256)],
+                                                                 dtype=torch.float64)), atol=1e-6)
+    assert torch.allclose(table[:, 0], torch.sin(p), atol=1e-4)
+    assert torch.allclose(table[:, 256], torch.cos(p), atol=1e-4)
+    assert torch.allclose(table[:, 255], torch.sin(p * 1e-4), atol=1e-6)
+    assert torch.allclose(table[:, 511], torch.cos(p * 1e-4), atol=1e-6)
+    assert math.isclose(float(table[0, 255]), math.sin(1e-4), rel_tol=1e-5)
+    freq = torch.tensor([10000.0 ** (-i / 255) for i in range(256)], dtype=torch.float64)
+    phase = p[:, None] * freq[None, :]
+    assert torch.allclose(table[:, :256], torch.sin(phase), atol=1e-4)
+    assert torch.allclose(table[:, 256:], torch.cos(phase), atol=1e-4)
+    assert torch.allclose(table[:, :256] ** 2 + table[:, 256:] ** 2, torch.ones(600, 256, dtype=torch.float64),
+                          atol=1e-6)

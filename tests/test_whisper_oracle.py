@@ -68,3 +68,34 @@ def test_decoder_steps_equal_prompt_pass():
         for p in range(6):
             step = model.model.decoder(tokens[:, p : p + 1], torch.full((2,), p), cache, None)
             assert max_rel_err(step[:, 0], full[:, p]) < 1e-10, p
+
+
+def test_suppress_masks_follow_the_config():
+    """whisper.py:536-544: the configured suppress_tokens and every token
+    after <|notimestamps|> are never chosen; the first step also suppresses
+    begin_suppress_tokens; a config without the lists suppresses only the
+    timestamps.  Checked element for element, and through the greedy choice
+    on logits that favour a suppressed token."""
+    vocab = ow.WHISPER_TINY["vocab_size"]
+    config = {"vocab_size": vocab, "suppress_tokens": [1, 2, 7, 50362], "begin_suppress_tokens": [220, 50257]}
+    suppress, first = ow.suppress_masks(config)
+    expected = torch.zeros(vocab, dtype=torch.bool)
+    expected[[1, 2, 7, 50362]] = True
+    expected[ow.NO_TIMESTAMPS + 1 :] = True
+    assert torch.equal(suppress, expected)
+    expected_first = expected.clone()
+    expected_first[[220, 50257]] = True
+    assert torch.equal(first, expected_first)
+    assert not suppress[ow.NO_TIMESTAMPS] and not suppress[220] and suppress[ow.NO_TIMESTAMPS + 1]
+
+    bare, bare_first = ow.suppress_masks({"vocab_size": vocab})
+    timestamps = torch.zeros(vocab, dtype=torch.bool)
+    timestamps[ow.NO_TIMESTAMPS + 1 :] = True
+    assert torch.equal(bare, timestamps) and torch.equal(bare_first, timestamps)
+
+    logits = torch.zeros(2, vocab)
+    logits[:, 7] = 5.0  # configured suppression: never chosen
+    logits[:, 220] = 4.0  # begin token: not chosen on the first step only
+    logits[:, 3] = 1.0
+    assert ow.choose(logits, suppress)[0].tolist() == [220, 220]
+    assert ow.choose(logits, first)[0].tolist() == [3, 3]
