@@ -63,19 +63,49 @@ struct Elem<bf16_raw> {
   static __device__ __forceinline__ void store1(bf16_raw* p, float x) { *p = f32_to_bf16(x); }
 };
 
+// The values of lanes l and l ^ OFF as a pair (a, b): a lane whose OFF bit
+// is clear gets its own value in a and its partner's in b (the partner gets
+// the same two values, in some order).  OFF 16 and 32 are one VALU lane swap
+// each (v_permlane16_swap, v_permlane32_swap: rows of 16 lanes, halves of
+// 32), OFF 8 a DPP rotation by 8 inside each row, which is l ^ 8; none goes
+// through the LDS crossbar as ds_bpermute does.
+template <int OFF>
+__device__ __forceinline__ void lane_pair(float x, float& a, float& b) {
+  static_assert(OFF == 8 || OFF == 16 || OFF == 32, "lane pair offset");
+  if constexpr (OFF == 32) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    a = __uint_as_float(r[0]);
+    b = __uint_as_float(r[1]);
+  } else if constexpr (OFF == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    a = __uint_as_float(r[0]);
+    b = __uint_as_float(r[1]);
+  } else {
+    a = x;
+    b = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xF, 0xF, false));  // row_ror:8
+  }
+}
+
 // Butterfly sum inside aligned groups of W lanes (W a power of two <= 64);
 // every lane of the group ends with the group's sum.  Steps within 16 lanes
 // use DPP (quad permutes, then half-row and row mirrors, which pair equal
-// partial sums once the smaller groups are summed); wider steps use
-// ds_bpermute.
+// partial sums once the smaller groups are summed); wider steps are lane
+// swaps (lane_pair).
 template <int W>
 __device__ __forceinline__ float group_sum(float x) {
   if constexpr (W >= 2) x += __builtin_amdgcn_update_dpp(0.f, x, 0xB1, 0xF, 0xF, false);   // quad_perm [1,0,3,2]
   if constexpr (W >= 4) x += __builtin_amdgcn_update_dpp(0.f, x, 0x4E, 0xF, 0xF, false);   // quad_perm [2,3,0,1]
   if constexpr (W >= 8) x += __builtin_amdgcn_update_dpp(0.f, x, 0x141, 0xF, 0xF, false);  // row_half_mirror
   if constexpr (W >= 16) x += __builtin_amdgcn_update_dpp(0.f, x, 0x140, 0xF, 0xF, false); // row_mirror
-#pragma unroll
-  for (int off = 16; off < W; off <<= 1) x += __shfl_xor(x, off, 64);
+  float a, b;
+  if constexpr (W >= 32) {
+    lane_pair<16>(x, a, b);
+    x = a + b;
+  }
+  if constexpr (W >= 64) {
+    lane_pair<32>(x, a, b);
+    x = a + b;
+  }
   return x;
 }
 
