@@ -336,17 +336,33 @@ __global__ __launch_bounds__(64 * RB * KS * DS, OCC) void fwd_ring_kernel(const 
   const int wlo = WIN && wrow0 < len_c ? first_key(p, sv, wlast) - kofs : 0;
   auto masked = [&](int kt) { return kt + BN > wmin || (WIN && kt < wlo); };
 
-  // S^T of tile j (stage stage_idx) into s.
+  // S^T of tile j (stage stage_idx) into s.  The K operands' LDS reads run
+  // two k-steps ahead of their matrix instructions; the scheduling groups
+  // pin that order (left alone, the compiler keeps one k-step's reads in
+  // flight, and the encoder lines measured 0.4-2% longer; three or four
+  // k-steps ahead cost Whisper large-v3-turbo 3-4%).
   auto qk = [&](int stage_idx, f32x16_t* s) {
     const uint32_t so = (uint32_t)stage_idx * SB;
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) s[kb] = f32x16_t{};
+    bf16x8_t kf[KST][KB];
 #pragma unroll
-    for (int kk = 0; kk < KST; ++kk) {
+    for (int kk = 0; kk < KST; ++kk)
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb)
-        s[kb] = mfma32(lds_read16(kaddr[kk % KA] + (kk / KA) * 256 + so + kb * 32 * RBYTES), qreg[kk], s[kb]);
+      for (int kb = 0; kb < KB; ++kb) kf[kk][kb] = lds_read16(kaddr[kk % KA] + (kk / KA) * 256 + so + kb * 32 * RBYTES);
+#pragma unroll
+    for (int kk = 0; kk < KST; ++kk)
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) s[kb] = mfma32(kf[kk][kb], qreg[kk], s[kb]);
+    constexpr int kAhead = KST < 2 ? KST : 2;
+    constexpr int kDsRead = 0x100, kMfma = 0x008;  // sched_group_barrier instruction classes
+    __builtin_amdgcn_sched_group_barrier(kDsRead, kAhead * KB, 0);
+#pragma unroll
+    for (int i = 0; i < KST - kAhead; ++i) {
+      __builtin_amdgcn_sched_group_barrier(kMfma, KB, 0);
+      __builtin_amdgcn_sched_group_barrier(kDsRead, KB, 0);
     }
+    __builtin_amdgcn_sched_group_barrier(kMfma, kAhead * KB, 0);
   };
   // Keys outside the row's [row_lo, row_lim) -> -inf.  Accumulator r of
   // block kb is key kt + 32 kb + 8 (r / 4) + 4 half + r % 4.
