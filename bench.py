@@ -106,6 +106,7 @@ class Workload:
     work_per_step: float  # flop or bytes
     peak: float = 0.0  # the roofline's peak; 0: bf16 MFMA for TFLOP/s, HBM for GB/s
     dtype: str = "bf16"
+    counters: bool = True  # whether --profile runs its counter passes
 
     def run(self) -> None:
         raise NotImplementedError
@@ -485,6 +486,9 @@ class Gemma4TextDecode(Workload):
     unit = "GB/s"
     bound = "hbm"
     kernel = "decode_kernel"
+    # Its 128-step schedule is ~8,100 dispatches, too many for a counter
+    # pass within the profiler run's time limit.
+    counters = False
 
     def __init__(self, torch, attention, seed: int = 6, steps: int = 128) -> None:
         rng = np.random.default_rng(seed)
@@ -1559,14 +1563,14 @@ def profile(out: Path, keys: list[str], steps: int, warmup: int) -> int:
         log(f"profile: {key} {tag} done (exit {rc})")
         return result, directory, shown
 
-    def counter(key: str, name: str) -> tuple[list[tuple[int, str, float]], str]:
-        _, directory, shown = child(key, name.lower(), ["--pmc", name], 2, 1)
-        return _dispatch_counters(directory, name), shown
+    def counter(key: str, name: str) -> tuple[list[tuple[int, str, float]], str, dict]:
+        result, directory, shown = child(key, name.lower(), ["--pmc", name], 2, 1)
+        return _dispatch_counters(directory, name), shown, result
 
     scale = {}
     calibration = {}
     for name in ("FETCH_SIZE", "WRITE_SIZE"):
-        values, shown = counter("copy", name)
+        values, shown, _ = counter("copy", name)
         kib = max(v for _, _, v in values)
         scale[name] = (1 << 30) / (kib * 1024.0)
         calibration[name] = {"kib_per_1GiB_copy": kib, "scale": round(scale[name], 4), "command": shown}
@@ -1598,12 +1602,15 @@ def profile(out: Path, keys: list[str], steps: int, warmup: int) -> int:
         per_step_us = sum(d for _, d in durations) / max(n_timed, 1)
         stats = sorted(_csv_rows(directory, "kernel_stats.csv"), key=lambda r: -float(r["TotalDurationNs"]))[:6]
 
-        traffic = {}
-        commands = {}
-        for name in ("FETCH_SIZE", "WRITE_SIZE"):
-            values, commands[name] = counter(key, name)
+        traffic = {"FETCH_SIZE": None, "WRITE_SIZE": None}
+        commands = {"FETCH_SIZE": "(no counter pass for this workload)", "WRITE_SIZE": ""}
+        counted = None  # a counter run's own result: the same steps as its counters
+        for name in ("FETCH_SIZE", "WRITE_SIZE") if cls.counters else ():
+            values, commands[name], counted = counter(key, name)
             mine = [v for _, kernel, v in values if cls.kernel in kernel]
-            mine = mine[-2 * cls_launches(plain):] or mine
+            # The counter run's timed steps: its last two, or a fixed
+            # schedule (Qwen3's 128 decode steps) whole.
+            mine = mine[-counted["steps_timed"] * cls_launches(plain):] or mine
             traffic[name] = statistics.mean(mine) * 1024.0 * scale[name] if mine else None
         short = short_kernel(kernel_name)
         entry = {"kernel": short, "launches_per_step": cls_launches(plain),
@@ -1612,9 +1619,11 @@ def profile(out: Path, keys: list[str], steps: int, warmup: int) -> int:
         entry["bytes_per_launch"] = (entry["fetch_bytes"] + entry["write_bytes"]
                                      if entry["fetch_bytes"] is not None and entry["write_bytes"] is not None
                                      else None)
-        if plain.get("work_per_launch") and plain["unit"] == "GB/s":
-            entry["algorithmic_bytes_per_launch"] = round(plain["work_per_launch"])
-        workloads[key] = entry
+        # Algorithmic bytes of the launches the counters saw.
+        if counted and counted.get("work_per_launch") and counted["unit"] == "GB/s":
+            entry["algorithmic_bytes_per_launch"] = round(counted["work_per_launch"])
+        if cls.counters:
+            workloads[key] = entry
 
         if cls.bound == "mfma":
             # One counter pass: matrix-core busy and VALU co-execution cycles,
@@ -1656,12 +1665,11 @@ def profile(out: Path, keys: list[str], steps: int, warmup: int) -> int:
             "",
             f"    {plain_cmd}",
             f"    {trace_cmd}",
-            f"    {commands['FETCH_SIZE']}",
-            f"    {commands['WRITE_SIZE']}",
+            *[f"    {c}" for c in (commands["FETCH_SIZE"], commands["WRITE_SIZE"]) if c],
             "",
             "| Figure | Value |",
             "|---|---|",
-            f"| bench, plain run: median ms per step ({steps} steps) | {plain['ms_per_step']} |",
+            f"| bench, plain run: median ms per step ({plain['steps_timed']} steps) | {plain['ms_per_step']} |",
             f"| bench, plain run: µs per launch of the dominant kernel (step ÷ {cls_launches(plain)}) | "
             f"{plain['ms_per_step'] * 1e3 / cls_launches(plain):.2f} |",
             f"| bench inside the traced run: median ms per step | {traced['ms_per_step']} |",
@@ -1673,10 +1681,13 @@ def profile(out: Path, keys: list[str], steps: int, warmup: int) -> int:
             f"(≤ {traced['ms_per_step_mean']} mean ms per step of the same run: "
             f"{'yes' if per_step_us / 1e3 <= traced['ms_per_step_mean'] * 1.001 else 'no'}) |",
             f"| FETCH_SIZE per launch (scaled ×{scale['FETCH_SIZE']:.3f}) | "
-            f"{entry['fetch_bytes'] / 1e6 if entry['fetch_bytes'] else float('nan'):.2f} MB |",
+            + (f"{entry['fetch_bytes'] / 1e6:.2f} MB |" if entry["fetch_bytes"] else "— |"),
             f"| WRITE_SIZE per launch (scaled ×{scale['WRITE_SIZE']:.3f}) | "
-            f"{entry['write_bytes'] / 1e6 if entry['write_bytes'] else float('nan'):.2f} MB |",
+            + (f"{entry['write_bytes'] / 1e6:.2f} MB |" if entry["write_bytes"] else "— |"),
         ]
+        if counted:
+            lines.append(f"| counter runs: steps timed (the counters' mean is over their launches) | "
+                         f"{counted['steps_timed']} |")
         if "algorithmic_bytes_per_launch" in entry:
             lines.append(f"| algorithmic bytes per launch | {entry['algorithmic_bytes_per_launch'] / 1e6:.2f} MB |")
         lines += ["", "Kernel stats of the traced run (every launch, warm-up and untimed runs included):", "",
@@ -1696,8 +1707,9 @@ def profile(out: Path, keys: list[str], steps: int, warmup: int) -> int:
     text = "\n".join([
         "# HBM traffic per launch of each workload's dominant kernel",
         "",
-        "FETCH_SIZE and WRITE_SIZE (KiB per dispatch, one rocprofv3 `--pmc` pass each, mean over the last two "
-        "steps' launches), scaled by what the same counter reads for a 1 GiB device copy "
+        "FETCH_SIZE and WRITE_SIZE (KiB per dispatch, one rocprofv3 `--pmc` pass each, mean over the launches "
+        "of the counter run's timed steps: its last two, or a fixed schedule whole), scaled by what the same "
+        "counter reads for a 1 GiB device copy "
         f"(FETCH ×{scale['FETCH_SIZE']:.3f}, WRITE ×{scale['WRITE_SIZE']:.3f}).  Made by "
         "`python3 bench.py --profile <dir>`; bench.py uses these figures only while the kernel sources hash "
         f"to `{digest}`.",
