@@ -56,6 +56,12 @@ struct DecodeShape {
   // 128 VGPRs.
   static constexpr int kUnroll = G >= 4 || HD >= 256 ? 2 : 4;
   static constexpr int kStep = kStreams * kUnroll;  // keys per load batch
+  // Plain (not append) kernels on 4-wave workgroups load two keys per
+  // stream per batch instead of four: Qwen3's paged step 4.71 -> 4.93 TB/s,
+  // its slab step +1%; the fused step lost 4% with two and keeps four.
+  // Slab and paged variants sum in the same order either way.
+  static constexpr int kPlainUnroll = W == 4 && kUnroll == 4 ? 2 : kUnroll;
+  static constexpr int kPlainStep = kStreams * kPlainUnroll;
   // Waves per SIMD the register budget allows: four (128 VGPRs) up to four
   // query heads per kv head, two (256) for eight.
   static constexpr int kOcc = G >= 8 ? 2 : 4;
@@ -303,15 +309,25 @@ struct Stream {
 // split folds them into its state); the first split writes them to the
 // cache at positions[b].  No workgroup reads that slot, so splits need no
 // ordering among themselves.
-template <typename T, int HD, int G, int W, bool APPEND, bool PAGED>
+//
+// SPEC (plain slab launches with one split, no window, key counts in
+// device memory and a cache of at least eight first batches; the launch
+// chooses it): the first load batch, keys 0 .. STEP - 1, is issued before
+// the row's key count is read, from buffer resources that end at the
+// cache's capacity; once the count is known, keys at or past it are masked
+// and their values zeroed (cache slots past a row's keys may hold anything).
+// The masked keys then add exactly zero, as the zeros of a resource ending
+// at the count do, so the output is the same bit for bit; the launch is
+// one round trip shorter at its start (Qwen3's step: 22.74 -> 22.37 us per
+// launch, same box).  The fused step (its prologue's loads already cover
+// that round trip) measured 2% slower with it and does not take it.
+template <typename T, int HD, int G, int W, bool APPEND, bool PAGED, bool SPEC = false>
 __global__ __launch_bounds__(64 * W, (DecodeShape<T, HD, G, W>::kOcc)) void decode_kernel(const DecodeArgs a) {
+  static_assert(!SPEC || (!APPEND && !PAGED), "speculative first batch: plain slab launches");
   using S = DecodeShape<T, HD, G, W>;
   constexpr int EPL = S::kEPL, LPK = S::kLPK, NS = S::kStreams;
-  // Keys per stream per load batch: the shape's, except two for plain
-  // (not append) kernels on 4-wave workgroups: Qwen3's paged step 4.71 ->
-  // 4.93 TB/s, its slab step +1%; the fused step lost 4% with two and keeps
-  // four.  Slab and paged variants sum in the same order either way.
-  constexpr int U = !APPEND && W == 4 && S::kUnroll == 4 ? 2 : S::kUnroll;
+  // Keys per stream per load batch.
+  constexpr int U = APPEND ? S::kUnroll : S::kPlainUnroll;
   constexpr int STEP = NS * U;
   const asrattn_decode_params& p = a.p;
 
@@ -337,9 +353,9 @@ __global__ __launch_bounds__(64 * W, (DecodeShape<T, HD, G, W>::kOcc)) void deco
   // q is used raw (no unpacking), so its load latency overlaps the first
   // K/V batch's; it and the prologue's inputs load before the key count is
   // read, which none of them needs (Qwen3's step 21.4 -> 20.9 us per launch,
-  // the fused step 23.1 -> 22.6).  Issuing the first K/V batch before the
-  // count as well (keys 0 .. STEP - 1 from a resource ending at max_len_k,
-  // masked afterwards) measured the same.
+  // the fused step 23.1 -> 22.6).  SPEC issues the first K/V batch there
+  // too; without the scheduling barrier below, the compiler moves the
+  // count's load and its wait above those loads.
   Stream<T, HD, G, W> st;
   {
     const T* qp = static_cast<const T*>(p.q) + (int64_t)b * p.q_batch_stride +
@@ -372,6 +388,21 @@ __global__ __launch_bounds__(64 * W, (DecodeShape<T, HD, G, W>::kOcc)) void deco
     kw = *reinterpret_cast<const uint4*>(kwp + sub * EPL);
     cs = *reinterpret_cast<const uint4*>(csp + sub * EPL);
     sn = *reinterpret_cast<const uint4*>(snp + sub * EPL);
+  }
+
+  // Two register batches in ping-pong: the next batch is in flight while the
+  // current one is consumed.
+  uint4 ka[U], va[U], kb[U], vb[U];
+  if constexpr (SPEC) {
+    const __amdgpu_buffer_rsrc_t kcap = buffer_rsrc(kbase, (uint32_t)p.max_len_k * kts);
+    const __amdgpu_buffer_rsrc_t vcap = buffer_rsrc(vbase, (uint32_t)p.max_len_k * vts);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t j = (uint32_t)(u * NS + stream);
+      ka[u] = buffer_load16_stream(kcap, j * kts + lane_bytes);
+      va[u] = buffer_load16_stream(vcap, j * vts + lane_bytes);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // the batch's issue stays above the count's load
   }
 
   const int64_t pos = APPEND ? p.positions[b] : 0;
@@ -430,13 +461,21 @@ __global__ __launch_bounds__(64 * W, (DecodeShape<T, HD, G, W>::kOcc)) void deco
     return mask;
   };
 
-  // Two register batches in ping-pong: the next batch is in flight while the
-  // current one is consumed.
   // The first batch is issued unconditionally: with k0 >= k1 its offsets all
-  // lie past the resource's end and read zeros.
-  uint4 ka[U], va[U], kb[U], vb[U];
+  // lie past the resource's end and read zeros.  SPEC's was issued above
+  // (k0 = 0 with one split and no window); it is masked here.
   unsigned mb = 0;
-  unsigned ma = load(ka, va, k0);
+  unsigned ma = 0;
+  if constexpr (SPEC) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const bool valid = u * NS + stream < k1;
+      ma |= (valid ? 1u : 0u) << u;
+      if (!valid) va[u] = make_uint4(0u, 0u, 0u, 0u);
+    }
+  } else {
+    ma = load(ka, va, k0);
+  }
   if constexpr (APPEND) {
     __builtin_amdgcn_sched_barrier(0);  // keep the prologue below the batch's issue
 #pragma unroll
@@ -568,12 +607,23 @@ hipError_t launch_typed(const DecodeArgs& a, bool append, hipStream_t stream) {
   const asrattn_decode_params& p = a.p;
   dim3 grid(a.splits, p.heads_kv, p.batch);
   const bool paged = a.pk.block_table != nullptr;
+  // Key counts read from device memory, one split, no window, and a cache
+  // of at least eight first batches: the first batch need not wait for the
+  // count (SPEC).  Its resource ends at the capacity, not at the count, so a
+  // batch as wide as the cache reads keys the row does not have: Whisper's
+  // self-attention over a 256-key bucket, one 256-key batch, read 2.3x its
+  // bytes and ran 3% slower with it.
+  constexpr int kFirstBatch = DecodeShape<T, HD, G, W>::kPlainStep;
+  const bool spec = !append && !paged && a.splits == 1 && p.window <= 0 &&
+                    (p.seqused_k != nullptr || p.positions != nullptr) && p.max_len_k >= 8 * kFirstBatch;
   if (append && paged)
     hipLaunchKernelGGL((decode_kernel<T, HD, G, W, true, true>), grid, dim3(64 * W), 0, stream, a);
   else if (append)
     hipLaunchKernelGGL((decode_kernel<T, HD, G, W, true, false>), grid, dim3(64 * W), 0, stream, a);
   else if (paged)
     hipLaunchKernelGGL((decode_kernel<T, HD, G, W, false, true>), grid, dim3(64 * W), 0, stream, a);
+  else if (spec)
+    hipLaunchKernelGGL((decode_kernel<T, HD, G, W, false, false, true>), grid, dim3(64 * W), 0, stream, a);
   else
     hipLaunchKernelGGL((decode_kernel<T, HD, G, W, false, false>), grid, dim3(64 * W), 0, stream, a);
   hipError_t err = hipGetLastError();
