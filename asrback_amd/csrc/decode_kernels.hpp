@@ -310,12 +310,14 @@ struct Stream {
 // cache at positions[b].  No workgroup reads that slot, so splits need no
 // ordering among themselves.
 //
-// SPEC (plain slab launches with one split, no window, key counts in
-// device memory and a cache of at least eight first batches; the launch
-// chooses it): the first load batch, keys 0 .. STEP - 1, is issued before
-// the row's key count is read, from buffer resources that end at the
-// cache's capacity; once the count is known, keys at or past it are masked
-// and their values zeroed (cache slots past a row's keys may hold anything).
+// SPEC (plain launches with one split, no window, key counts in device
+// memory and a cache of at least eight first batches; paged, a first page
+// that holds the whole first batch; the launch chooses it): the first load
+// batch, keys 0 .. STEP - 1, is issued before the row's key count is read,
+// from buffer resources that end at the cache's capacity (paged: at the
+// first page's end, the page read from the block table meanwhile); once the
+// count is known, keys at or past it are masked and their values zeroed
+// (cache slots past a row's keys may hold anything).
 // The masked keys then add exactly zero, as the zeros of a resource ending
 // at the count do, so the output is the same bit for bit; the launch is
 // one round trip shorter at its start (Qwen3's step: 22.74 -> 22.37 us per
@@ -323,7 +325,7 @@ struct Stream {
 // that round trip) measured 2% slower with it and does not take it.
 template <typename T, int HD, int G, int W, bool APPEND, bool PAGED, bool SPEC = false>
 __global__ __launch_bounds__(64 * W, (DecodeShape<T, HD, G, W>::kOcc)) void decode_kernel(const DecodeArgs a) {
-  static_assert(!SPEC || (!APPEND && !PAGED), "speculative first batch: plain slab launches");
+  static_assert(!SPEC || !APPEND, "speculative first batch: plain launches");
   using S = DecodeShape<T, HD, G, W>;
   constexpr int EPL = S::kEPL, LPK = S::kLPK, NS = S::kStreams;
   // Keys per stream per load batch.
@@ -393,9 +395,31 @@ __global__ __launch_bounds__(64 * W, (DecodeShape<T, HD, G, W>::kOcc)) void deco
   // Two register batches in ping-pong: the next batch is in flight while the
   // current one is consumed.
   uint4 ka[U], va[U], kb[U], vb[U];
+  // Paged: pool page of logical page pi of this sequence, or -1 when the
+  // entry is missing or outside the pool (its keys are skipped).
+  const int32_t* bt = PAGED ? a.pk.block_table + (int64_t)b * a.pk.bt_stride : nullptr;
+  auto pool_page = [&](int pi) -> int {
+    if (pi >= a.pk.bt_stride) return -1;
+    const int e = bt[__builtin_amdgcn_readfirstlane(pi)];
+    return e >= 0 && e < a.pk.num_pages ? e : -1;
+  };
+
+  int page0 = 0;  // SPEC, paged: the sequence's first pool page (-1: none)
   if constexpr (SPEC) {
-    const __amdgpu_buffer_rsrc_t kcap = buffer_rsrc(kbase, (uint32_t)p.max_len_k * kts);
-    const __amdgpu_buffer_rsrc_t vcap = buffer_rsrc(vbase, (uint32_t)p.max_len_k * vts);
+    // Slab: resources up to the cache's capacity.  Paged: over the first
+    // page (the launch makes sure the batch fits in one).
+    const char* kp = kbase;
+    const char* vp = vbase;
+    uint32_t keys = (uint32_t)p.max_len_k;
+    if constexpr (PAGED) {
+      page0 = pool_page(0);
+      const int64_t pg = page0 >= 0 ? page0 : 0;
+      kp = kbase + pg * a.pk.k_page_stride * (int64_t)sizeof(T);
+      vp = vbase + pg * a.pk.v_page_stride * (int64_t)sizeof(T);
+      keys = page0 >= 0 ? (uint32_t)a.pk.page_size : 0u;
+    }
+    const __amdgpu_buffer_rsrc_t kcap = buffer_rsrc(kp, keys * kts);
+    const __amdgpu_buffer_rsrc_t vcap = buffer_rsrc(vp, keys * vts);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const uint32_t j = (uint32_t)(u * NS + stream);
@@ -424,15 +448,6 @@ __global__ __launch_bounds__(64 * W, (DecodeShape<T, HD, G, W>::kOcc)) void deco
   // the loop.  (Paged: the pool, past the sequence's first page.)
   const __amdgpu_buffer_rsrc_t krs = buffer_rsrc(kbase, (uint32_t)k1 * kts);
   const __amdgpu_buffer_rsrc_t vrs = buffer_rsrc(vbase, (uint32_t)k1 * vts);
-
-  // Paged: pool page of logical page pi of this sequence, or -1 when the
-  // entry is missing or outside the pool (its keys are skipped).
-  const int32_t* bt = PAGED ? a.pk.block_table + (int64_t)b * a.pk.bt_stride : nullptr;
-  auto pool_page = [&](int pi) -> int {
-    if (pi >= a.pk.bt_stride) return -1;
-    const int e = bt[__builtin_amdgcn_readfirstlane(pi)];
-    return e >= 0 && e < a.pk.num_pages ? e : -1;
-  };
 
   // Key u of the batch starting at `base` is base + u * NS + stream.
   auto load = [&](uint4* kr, uint4* vr, int base) -> unsigned {
@@ -469,7 +484,7 @@ __global__ __launch_bounds__(64 * W, (DecodeShape<T, HD, G, W>::kOcc)) void deco
   if constexpr (SPEC) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const bool valid = u * NS + stream < k1;
+      const bool valid = u * NS + stream < k1 && page0 >= 0;
       ma |= (valid ? 1u : 0u) << u;
       if (!valid) va[u] = make_uint4(0u, 0u, 0u, 0u);
     }
@@ -614,12 +629,15 @@ hipError_t launch_typed(const DecodeArgs& a, bool append, hipStream_t stream) {
   // self-attention over a 256-key bucket, one 256-key batch, read 2.3x its
   // bytes and ran 3% slower with it.
   constexpr int kFirstBatch = DecodeShape<T, HD, G, W>::kPlainStep;
-  const bool spec = !append && !paged && a.splits == 1 && p.window <= 0 &&
-                    (p.seqused_k != nullptr || p.positions != nullptr) && p.max_len_k >= 8 * kFirstBatch;
+  const bool spec = !append && a.splits == 1 && p.window <= 0 &&
+                    (p.seqused_k != nullptr || p.positions != nullptr) && p.max_len_k >= 8 * kFirstBatch &&
+                    (!paged || a.pk.page_size >= kFirstBatch);
   if (append && paged)
     hipLaunchKernelGGL((decode_kernel<T, HD, G, W, true, true>), grid, dim3(64 * W), 0, stream, a);
   else if (append)
     hipLaunchKernelGGL((decode_kernel<T, HD, G, W, true, false>), grid, dim3(64 * W), 0, stream, a);
+  else if (paged && spec)
+    hipLaunchKernelGGL((decode_kernel<T, HD, G, W, false, true, true>), grid, dim3(64 * W), 0, stream, a);
   else if (paged)
     hipLaunchKernelGGL((decode_kernel<T, HD, G, W, false, true>), grid, dim3(64 * W), 0, stream, a);
   else if (spec)
