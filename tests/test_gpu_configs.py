@@ -362,6 +362,58 @@ def test_decode_ignores_cache_slots_past_each_row(ops, device, dtype, hd, heads_
     assert torch.equal(kd.cpu()[rows, positions], k_new) and torch.equal(vd.cpu()[rows, positions], v_new)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_decode_speculative_first_batch_ignores_slots_past_each_row(ops, device, dtype):
+    """At the Qwen3 shape (64 rows x 8 kv heads of 128 over a 1024-slot
+    cache: one split) the first load batch (32 keys per workgroup) is
+    issued before the row's key count is read, over the whole cache's
+    extent.  Slots at and past each row's count hold NaN and +-inf; lengths
+    0, 1, 31, 32, 33 (around that batch) and 1023 among random ones.  The
+    outputs equal the oracle's over each row's own keys, the empty row gives
+    zeros, and a graph replay with other counts agrees with an eager call."""
+    say("decode speculative first batch", dtype)
+    batch, length, heads_q, heads_kv, hd = 64, 1024, 16, 8, 128
+    rng = np.random.default_rng(91)
+    lengths = rng.integers(1, length, size=batch)
+    lengths[:6] = [0, 1, 31, 32, 33, 1023]
+    n = torch.from_numpy(lengths)
+    q = randn(batch, heads_q, hd, seed=92, dtype=dtype)
+    keys = randn(batch, length, heads_kv, hd, seed=93, dtype=dtype)
+    values = randn(batch, length, heads_kv, hd, seed=94, dtype=dtype)
+    past = torch.arange(length)[None, :] >= n[:, None]
+    garbage = torch.tensor([float("nan"), float("inf"), -float("inf")])[torch.arange(length) % 3]
+    keys_bad, values_bad = keys.clone(), values.clone()
+    keys_bad[past] = garbage.expand(batch, length)[past][:, None, None].to(dtype)
+    values_bad[past] = garbage.expand(batch, length)[past].flip(0)[:, None, None].to(dtype)
+    mask = torch.arange(length)[None, :] < n[:, None]
+    ref = oa.qwen_step_attention(q.float(), keys.float(), values.float(), mask[:, None, None, :])
+    qd, kd, vd = q.to(device), keys_bad.to(device), values_bad.to(device)
+    used = n.to(torch.int32).to(device)
+    out = ops.decode(qd, kd, vd, seqused_k=used)
+    assert torch.isfinite(out).all()
+    assert torch.count_nonzero(out[0]) == 0
+    assert_close(out[1:].float().cpu(), ref[1:], KIND[dtype])
+
+    # Positions instead of counts (keys 0..positions[b]), replayed from a graph.
+    positions = (n - 1).clamp(min=0).to(torch.int64).to(device)
+    static_out = torch.empty_like(out)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        ops.decode(qd, kd, vd, positions=positions, out=static_out)
+    torch.cuda.current_stream().wait_stream(stream)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        ops.decode(qd, kd, vd, positions=positions, out=static_out)
+    for shift in (0, -7, -20):  # within each row's own keys
+        positions.copy_(((n - 1 + shift).clamp(0, length - 1)).to(torch.int64).to(device))
+        graph.replay()
+        torch.cuda.synchronize()
+        eager = ops.decode(qd, kd, vd, positions=positions)
+        assert torch.equal(static_out, eager), shift
+        assert torch.isfinite(static_out).all()
+
+
 def test_encoder_zero_keys_gives_zeros(ops, device):
     q = randn(2, 40, 2, 128, seed=34, dtype=torch.bfloat16).to(device)
     used = torch.tensor([0, 17], dtype=torch.int32, device=device)
