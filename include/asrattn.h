@@ -172,7 +172,10 @@ int asrattn_fwd_fsmn(const asrattn_fwd_params* params, const asrattn_fsmn_params
  * k/v token t of sequence b, head h is at k + b*k_batch_stride +
  * t*k_token_stride + h*k_head_stride: both cache layouts of the reference
  * are plain strides, (batch, heads, length, head_dim) for Whisper and
- * (batch, 1024, kv_heads, head_dim) for Qwen3-ASR.
+ * (batch, 1024, kv_heads, head_dim) for Qwen3-ASR.  Tokens 0 .. max_len_k - 1
+ * of every sequence must be readable memory: the first load batch may be
+ * issued before n_b is read and may touch tokens at or past n_b, which are
+ * then discarded whatever they hold (NaN and infinities included).
  *
  * workspace: device memory of asrattn_decode_workspace_size(params) bytes
  * (0 when a single split is used), 256-byte aligned, owned by the caller;
@@ -312,8 +315,10 @@ int asrattn_decode_append(const asrattn_decode_params* params, const asrattn_app
  * asrattn_decode_append (the new key and value are written to the page of
  * positions[b]); the workspace size is asrattn_decode_workspace_size's.
  * max_len_k bounds the keys a sequence may use (<= bt_stride * page_size).
- * Only the entries of pages holding a sequence's keys are read; an entry
- * outside [0, num_pages) is not dereferenced and its keys are skipped.
+ * Only entry 0 and the entries of pages holding a sequence's keys are read;
+ * an entry outside [0, num_pages) is not dereferenced and its keys are
+ * skipped.  The first page's tokens may be read past n_b (the first load
+ * batch can be issued before n_b is read) and are then discarded.
  *
  * Replaces (generalizes): the flattened (B * 1024, kv_heads, head_dim) slab
  * with cu_seqlens_k = row * 1024 of the reference's varlen decode
